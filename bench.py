@@ -1,0 +1,285 @@
+"""Benchmark of the Dion optimizer step on one MI355X.
+
+Default workload: one full ``Dion.step()`` over
+Llama-3-8B-shaped float32 parameters — 32 layers of q/o 4096x4096, k/v
+1024x4096, gate/up 14336x4096, down 4096x14336 on Dion with fraction 0.25,
+embedding and lm_head 128256x4096 plus the RMSNorm weights on AdamW — with
+synthetic weights ~0.02 N(0,1) and gradients ~1e-3 N(0,1) resident in HBM.
+
+Prints one JSON line: the step time (``value``, ms), the Gram Newton-Schulz
+TFLOP/s and momentum-pass GB/s measured live with HIP events on the stream
+the kernels run on, the roofline of the dominant kernel family (the
+Newton-Schulz MFMA products) and the CPU oracle's time on a bounded sample.
+
+Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from collections import defaultdict
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense fp16/bf16
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+LLAMA = {
+    "layers": 32,
+    "matrices": [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+                 ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)],
+    "vocab": 128256,
+    "hidden": 4096,
+}
+GPT2 = {
+    "layers": 12,
+    "matrices": [("qkv", 2304, 768), ("proj", 768, 768), ("fc", 3072, 768), ("fc2", 768, 3072)],
+    "vocab": 50257,
+    "hidden": 768,
+}
+
+
+def ns_flops(kind: int, r: int, c: int) -> float:
+    """Algorithmic FLOPs of one Newton-Schulz block r x c (r <= c): the Gram
+    iteration 6 r^2 c + 23 r^3, the standard / quintic 15 r^2 c + 5 r^3."""
+    if kind == 0 and c > r:
+        return 6.0 * r * r * c + 23.0 * r**3
+    return 15.0 * r * r * c + 5.0 * r**3
+
+
+class Timeline:
+    """HIP-event timing of the library's entry points (instrumented steps only)."""
+
+    def __init__(self) -> None:
+        import torch
+
+        self.torch = torch
+        self.events: list[tuple[str, dict, object, object]] = []
+
+    def wrap(self, lib_module) -> None:
+        original = lib_module.call
+        torch = self.torch
+
+        def timed(name, *args):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            original(name, *args)
+            end.record()
+            self.events.append((name, {"args": args}, start, end))
+
+        lib_module.call = timed
+        self._restore = (lib_module, original)
+
+    def unwrap(self) -> None:
+        module, original = self._restore
+        module.call = original
+
+    def summary(self) -> dict[str, dict[str, float]]:
+        self.torch.cuda.synchronize()
+        out: dict[str, dict[str, float]] = defaultdict(lambda: {"ms": 0.0, "calls": 0, "flops": 0.0,
+                                                                 "bytes": 0.0})
+        for name, meta, start, end in self.events:
+            entry = out[name]
+            entry["ms"] += start.elapsed_time(end)
+            entry["calls"] += 1
+            a = meta["args"]
+            if name == "dionw_newton_schulz":
+                kind, batch, r_real, c_real = a[0], a[1], a[6], a[7]
+                entry["flops"] += batch * ns_flops(kind, r_real, c_real)
+            elif name == "dionw_accumulate_scores":
+                count, rows, cols = a[1], a[2], a[3]
+                entry["bytes"] += 12.0 * count * rows * cols
+            elif name == "dionw_prepare_ns_input":
+                blocks, cols, k = a[5], a[7], a[8]
+                entry["bytes"] += 12.0 * blocks * k * cols
+            elif name == "dionw_apply_update":
+                count, bpt, rows, cols, k, decay_on = a[1], a[2], a[3], a[4], a[5], a[13]
+                n = count * bpt * rows * cols
+                s = count * bpt * k * cols
+                entry["bytes"] += (8.0 * n if decay_on else 8.0 * s) + 2.0 * s
+            elif name == "dionw_adamw":
+                entry["bytes"] += 28.0 * sum(a[5][i] for i in range(a[6]))
+        return dict(out)
+
+
+def build_llama(torch, dev, spec, fraction):
+    g = torch.Generator(device=dev).manual_seed(0)
+    hidden = spec["hidden"]
+
+    def param(*shape):
+        p = torch.nn.Parameter(torch.empty(*shape, device=dev).normal_(0.0, 0.02, generator=g))
+        p.grad = torch.empty_like(p).normal_(0.0, 1e-3, generator=g)
+        return p
+
+    matrices, norms = [], []
+    for _ in range(spec["layers"]):
+        for _, rows, cols in spec["matrices"]:
+            matrices.append(param(rows, cols))
+        norms.extend([param(hidden), param(hidden)])
+    norms.append(param(hidden))
+    embed = [param(spec["vocab"], hidden), param(spec["vocab"], hidden)]
+    groups = [
+        {"params": embed, "dion_route": "adamw"},
+        {"params": norms, "dion_route": "adamw", "weight_decay": 0.0},
+        {"params": matrices, "dion_route": "matrix", "fraction": fraction},
+    ]
+    n_params = sum(p.numel() for grp in groups for p in grp["params"])
+    return groups, n_params
+
+
+def cpu_baseline(spec, fraction: float, threads: int) -> dict:
+    """The CPU oracle on one decoder layer's Dion blocks plus 1/layers of the
+    AdamW elements, scaled by the layer count (labelled extrapolated)."""
+    import numpy as np
+    import torch
+
+    from oracle import dion_ref
+
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    blocks = []
+    for _, rows, cols in spec["matrices"]:
+        w = torch.randn(1, rows, cols, generator=g) * 0.02
+        blocks.append((w, torch.randn(1, rows, cols, generator=g) * 1e-3, torch.zeros_like(w),
+                       torch.zeros(1, rows, 1), rows))
+    adamw_numel = (2 * spec["vocab"] * spec["hidden"]) // spec["layers"] + 2 * spec["hidden"]
+    rng = np.random.default_rng(0)
+    ap = (rng.standard_normal(adamw_numel) * 0.02).astype(np.float32)
+    ag = (rng.standard_normal(adamw_numel) * 1e-3).astype(np.float32)
+    am, av = np.zeros_like(ap), np.zeros_like(ap)
+
+    def one_layer(step: int) -> None:
+        for w, grad, m, v, rows in blocks:
+            k = min(rows, math.ceil(fraction * rows))
+            dion_ref.step_blocks(w, grad, m, v, k=k, lr=3e-4, mu=0.95, beta2=0.95,
+                                 weight_decay=0.05, kind="gram")
+        dion_ref.adamw(ap, ag, am, av, float(step), lr=3e-4, beta1=0.9, beta2=0.95,
+                       weight_decay=0.05, eps=1e-8)
+
+    t0 = time.perf_counter()
+    one_layer(1)
+    per_layer = time.perf_counter() - t0
+    return {
+        "value": per_layer * spec["layers"] * 1e3,
+        "unit": "ms/step (extrapolated)",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle (torch CPU restatement) on 1 of {spec['layers']} layers' Dion blocks "
+                  f"+ 1/{spec['layers']} of the AdamW elements, x{spec['layers']}",
+        "sample_seconds": round(per_layer, 2),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=5)
+    parser.add_argument("--warmup", type=int, default=2)
+    parser.add_argument("--config", default="llama3-8b", choices=["llama3-8b", "gpt2-small"])
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--instrumented-steps", type=int, default=2)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the optimizer step is single-device); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import dionw_amd
+    from dionw_amd import _lib
+
+    dev = torch.device("cuda:0")
+    spec = LLAMA if args.config == "llama3-8b" else GPT2
+    fraction = 0.25
+    print(f"[bench] building {args.config} parameters", file=sys.stderr, flush=True)
+    groups, n_params = build_llama(torch, dev, spec, fraction)
+    opt = dionw_amd.Dion(groups, lr=3e-4, weight_decay=0.05, momentum=0.95, muon_beta2=0.95,
+                         betas=(0.9, 0.95), eps=1e-8)
+    torch.cuda.synchronize()
+    print(f"[bench] {n_params / 1e9:.2f} G params; warmup {args.warmup}", file=sys.stderr,
+          flush=True)
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
+    host_t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        opt.step()
+    end.record()
+    host_dispatch = (time.perf_counter() - host_t0) / args.steps * 1e3
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+
+    timeline = Timeline()
+    timeline.wrap(_lib)
+    for _ in range(args.instrumented_steps):
+        opt.step()
+    summary = timeline.summary()
+    timeline.unwrap()
+    div = max(args.instrumented_steps, 1)
+    ns = summary.get("dionw_newton_schulz", {"ms": 0.0, "flops": 0.0, "calls": 0})
+    ns_tflops = ns["flops"] / (ns["ms"] * 1e-3) / 1e12 if ns["ms"] else 0.0
+    acc = summary.get("dionw_accumulate_scores", {"ms": 0.0, "bytes": 0.0})
+    acc_gbs = acc["bytes"] / (acc["ms"] * 1e-3) / 1e9 if acc["ms"] else 0.0
+    phases = {name: {"ms_per_step": round(v["ms"] / div, 3), "calls_per_step": v["calls"] // div,
+                     **({"tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1)} if v["flops"] else {}),
+                     **({"gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)} if v["bytes"] else {})}
+              for name, v in sorted(summary.items(), key=lambda kv: -kv[1]["ms"])}
+    print(f"[bench] phases {json.dumps(phases)}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(spec, fraction, threads=min(os.cpu_count() or 1, 16))
+
+    line = {
+        "metric": "Dion step ms at Llama-3-8B shapes" if args.config == "llama3-8b"
+        else "Dion step ms at GPT-2-small shapes",
+        "value": round(ms, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 state, f16/bf16 MFMA Newton-Schulz",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: full Dion step (Dion f={fraction} on every linear, "
+                        "AdamW on embeddings/lm_head/norms), fp32 params resident in HBM",
+            "params": n_params,
+        },
+        "gram_ns_tflops": round(ns_tflops, 1),
+        "momentum_pass_gbs": round(acc_gbs, 1),
+        "host_dispatch_ms": round(host_dispatch, 3),
+        "phases": phases,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_nt_kernel (Newton-Schulz products)",
+            "achieved": round(ns_tflops, 1),
+            "peak": PEAK_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(ns_tflops / PEAK_MFMA_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(ns["ms"] * 1e3 / max(ns.get("calls", 0), 1), 1),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

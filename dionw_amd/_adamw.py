@@ -1,0 +1,92 @@
+"""The AdamW route on the multi-tensor HIP kernel.
+
+Reference: src/dionw/_adamw.py:18-61 (``torch._fused_adamw_`` with a float32
+0-d device step counter per parameter). The step counters are incremented on
+the device by one launch, then one launch per 48 tensors applies AdamW with
+ATen's arithmetic, so results are bit-identical to torch's fused AdamW.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from dionw_amd import _lib
+from dionw_amd._keys import ADAMW_STEP_STATE, EXP_AVG_SQ_STATE, EXP_AVG_STATE, ParamState
+
+__all__ = ["adamw_step", "init_adamw_state"]
+
+
+def init_adamw_state(param: Tensor, state: dict[str, Any]) -> None:
+    """Fresh AdamW moments and step counter in ``state``."""
+    state[EXP_AVG_STATE] = torch.zeros_like(param)
+    state[EXP_AVG_SQ_STATE] = torch.zeros_like(param)
+    state[ADAMW_STEP_STATE] = torch.zeros((), dtype=torch.float32, device=param.device)
+
+
+def _dense_like(tensor: Tensor, reference: Tensor) -> bool:
+    return tensor.stride() == reference.stride() and tensor.is_non_overlapping_and_dense()
+
+
+def adamw_step(group: dict[str, Any], state: ParamState) -> None:
+    """One AdamW step of the group's parameters that have gradients.
+
+    Raises:
+        RuntimeError: If a gradient disappears between selection and the step.
+        TypeError: For a parameter that is not float32.
+    """
+    params = [p for p in group["params"] if p.grad is not None]
+    if not params:
+        return
+    entries = [state[p] for p in params]
+    targets: list[Tensor] = []
+    grads: list[Tensor] = []
+    exp_avgs: list[Tensor] = []
+    exp_avg_sqs: list[Tensor] = []
+    copies: list[tuple[Tensor, Tensor]] = []
+    for param, entry in zip(params, entries, strict=True):
+        if EXP_AVG_STATE not in entry:
+            init_adamw_state(param, entry)
+        grad = param.grad
+        if grad is None:
+            raise RuntimeError("an AdamW update holds a parameter without a gradient")
+        if param.dtype != torch.float32:
+            raise TypeError(f"the HIP AdamW takes float32 parameters, got {param.dtype}")
+        data = param.data
+        m, v = entry[EXP_AVG_STATE], entry[EXP_AVG_SQ_STATE]
+        grad = grad.to(torch.float32)
+        if not (data.is_non_overlapping_and_dense() and all(_dense_like(t, data) for t in (grad, m, v))):
+            # Mixed layouts: step row-major copies and write them back.
+            flat = [t.contiguous() for t in (data, m, v)]
+            copies.extend(zip((data, m, v), flat, strict=True))
+            data, m, v = flat
+            grad = grad.contiguous()
+        targets.append(data)
+        grads.append(grad)
+        exp_avgs.append(m)
+        exp_avg_sqs.append(v)
+    steps = [entry[ADAMW_STEP_STATE] for entry in entries]
+    stream = _lib.stream_handle(params[0].device)
+    _lib.call("dionw_increment_steps", _lib.ptr_array(steps), len(steps), stream)
+    beta1, beta2 = group["betas"]
+    _lib.call(
+        "dionw_adamw",
+        _lib.ptr_array(targets),
+        _lib.ptr_array(grads),
+        _lib.ptr_array(exp_avgs),
+        _lib.ptr_array(exp_avg_sqs),
+        _lib.ptr_array(steps),
+        _lib.int64_array([t.numel() for t in targets]),
+        len(targets),
+        float(group["lr"]),
+        float(beta1),
+        float(beta2),
+        float(group["weight_decay"]),
+        float(group["eps"]),
+        stream,
+    )
+    for original, copy in copies:
+        if original.data_ptr() != copy.data_ptr():
+            original.copy_(copy)

@@ -1,0 +1,191 @@
+"""One Dion step for a run of consecutive bucket parameters with gradients.
+
+Reference: src/dionw/_matrix_step.py:104-311. Per block:
+
+1. accumulate ``M += G`` (with each row's l1 score when rows are selected);
+2. select the top ``k`` rows and decay them in ``M`` (error feedback), or, when
+   every row is updated, ``M = mu (M + G)`` with the heavy-ball or Nesterov
+   input;
+3. orthogonalize the selected (or all) rows;
+4. NorMuon row normalization, or none, times the signed step;
+5. decoupled weight decay on every row, then the update on the selected rows.
+
+On the HIP path this is five to seven launches per run, each over the whole
+run through pointer tables: accumulate/sumsq, select, prepare (decay + the
+normalized 16-bit input in both orientations), the Newton-Schulz products,
+NorMuon statistics and the fused apply. A user-supplied orthogonalization
+(``newton_schulz_fn`` replaced) receives the float32 input rows instead, as
+the reference's plugin does.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any, Final
+
+import torch
+from torch import Tensor
+
+from dionw_amd import _lib, _workspace
+from dionw_amd._buckets import Bucket
+from dionw_amd._keys import (
+    MOMENTUM_FORM_KEY,
+    MOMENTUM_KEY,
+    MUON_BETA2_KEY,
+    ROW_NORMALIZATION_KEY,
+    ParamState,
+)
+from dionw_amd.matrix_update import MomentumForm, RowNormalization
+from dionw_amd.newton_schulz import HipOrthogonalize, run_newton_schulz
+
+__all__ = ["MAX_RUN_ELEMENTS", "run_elements", "step_run"]
+
+# AdamW update RMS that matrix steps match (Moonshot's 0.2).
+ADAMW_UPDATE_RMS: Final[float] = 0.2
+# Added to the Frobenius norm before Newton-Schulz.
+NEWTON_SCHULZ_EPS: Final[float] = 1e-8
+# Largest update (blocks x selected rows x cols) one run orthogonalizes at once.
+MAX_RUN_ELEMENTS: Final[int] = 2**28
+
+
+def run_elements(bucket: Bucket, position: int) -> int:
+    """Update elements of the parameter at ``position`` of ``bucket``."""
+    blocks = bucket.slices[position]
+    return (blocks.stop - blocks.start) * bucket.selected_rows * bucket.cols
+
+
+@dataclass
+class _Run:
+    bucket: Bucket
+    params: list[Tensor]        # contiguous parameter storage the kernels write
+    writeback: list[tuple[Tensor, Tensor]]  # (parameter, contiguous copy) to copy back
+    grads: list[Tensor]         # contiguous float32 gradients
+    momentum: Tensor            # [blocks, rows, cols]
+    variance: Tensor            # [blocks, rows, 1]
+
+    @property
+    def blocks(self) -> int:
+        return int(self.momentum.shape[0])
+
+
+def _make_run(bucket: Bucket, positions: list[int] | range) -> _Run:
+    params: list[Tensor] = []
+    writeback: list[tuple[Tensor, Tensor]] = []
+    grads: list[Tensor] = []
+    for i in positions:
+        param = bucket.params[i]
+        grad = param.grad
+        if grad is None:
+            raise RuntimeError("a Dion run holds a parameter without a gradient")
+        # Channels-last (or otherwise strided) tensors go through row-major copies.
+        grads.append(grad.to(torch.float32).contiguous())
+        if param.is_contiguous():
+            params.append(param.data)
+        else:
+            copy = param.data.contiguous()
+            params.append(copy)
+            writeback.append((param.data, copy))
+    blocks = bucket.run_blocks(list(positions))
+    return _Run(bucket, params, writeback, grads, bucket.momentum[blocks],
+                bucket.variance[blocks])
+
+
+def _step_size(bucket: Bucket, lr: float) -> float:
+    """lr times AdamW's update RMS times the Frobenius compensation of a
+    partial-row step (_matrix_step.py:147-159)."""
+    rows, cols, k = bucket.rows, bucket.cols, bucket.selected_rows
+    return lr * ADAMW_UPDATE_RMS * math.sqrt(max(rows, cols)) * math.sqrt(
+        min(rows, cols) / min(k, cols)
+    )
+
+
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+def step_run(
+    bucket: Bucket, positions: list[int] | range, group: dict[str, Any], state: ParamState
+) -> None:
+    """Apply one Dion step to the consecutive bucket parameters ``positions``.
+
+    Raises:
+        RuntimeError: If a parameter has no gradient.
+    """
+    del state  # the run's momentum and variance are views of the bucket
+    run = _make_run(bucket, positions)
+    lr = float(group["lr"])
+    step = -_step_size(bucket, lr)
+    device = run.momentum.device
+    stream = _lib.stream_handle(device)
+    blocks, rows, cols, k = run.blocks, bucket.rows, bucket.cols, bucket.selected_rows
+    count = len(run.grads)
+    per_param = bucket.blocks_per_param
+    mu = float(group[MOMENTUM_KEY])
+    nesterov = MomentumForm(group[MOMENTUM_FORM_KEY]) is MomentumForm.NESTEROV
+    ortho = bucket.orthogonalize
+    fused = isinstance(ortho, HipOrthogonalize)
+    safety = ortho.norm_safety if fused else 1.0
+    grads = _lib.ptr_array(run.grads)
+    momentum = run.momentum
+
+    den = _workspace.buffer(device, "den", (blocks,), torch.float32)
+    rowsq = _workspace.buffer(device, "rowsq", (blocks * rows,), torch.float32)
+    selected = k < rows
+    idx = slot = None
+    if selected:
+        scores = _workspace.buffer(device, "scores", (blocks * rows,), torch.float32)
+        idx = _workspace.buffer(device, "idx", (blocks, k), torch.int32)
+        slot = _workspace.buffer(device, "slot", (blocks, rows), torch.int32)
+        _lib.call("dionw_accumulate_scores", grads, count, per_param * rows, cols,
+                  momentum.data_ptr(), scores.data_ptr(), rowsq.data_ptr(), stream)
+        _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k,
+                  safety, NEWTON_SCHULZ_EPS, idx.data_ptr(), slot.data_ptr(), den.data_ptr(),
+                  stream)
+    elif fused:
+        _lib.call("dionw_full_sumsq", grads, count, per_param * rows, cols, momentum.data_ptr(),
+                  mu, int(nesterov), rowsq.data_ptr(), stream)
+        _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, safety, NEWTON_SCHULZ_EPS,
+                  den.data_ptr(), stream)
+    idx_ptr = None if idx is None else idx.data_ptr()
+
+    if fused:
+        p_pad, j_pad = _round8(k), _round8(cols)
+        xr = _workspace.buffer(device, "ns_xr", (blocks, p_pad, j_pad), ortho.dtype)
+        xt = _workspace.buffer(device, "ns_xt", (blocks, j_pad, p_pad), ortho.dtype)
+        _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
+                  den.data_ptr(), blocks, rows, cols, k, p_pad, j_pad, mu, int(nesterov), 1,
+                  ortho.elem, xr.data_ptr(), xt.data_ptr(), stream)
+        orthogonal = _workspace.buffer(device, "ns_out", (blocks, k, cols), torch.bfloat16)
+        run_newton_schulz(ortho, blocks, k, cols, xr, xt, orthogonal, stream)
+    else:
+        raw = torch.empty(blocks, k, cols, device=device, dtype=torch.float32)
+        _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
+                  den.data_ptr(), blocks, rows, cols, k, k, cols, mu, int(nesterov), 1,
+                  _lib.F32, raw.data_ptr(), None, stream)
+        orthogonal = ortho(raw, NEWTON_SCHULZ_EPS)
+        orthogonal = orthogonal.to(torch.bfloat16).contiguous()
+
+    rowd = scale = None
+    match RowNormalization(group[ROW_NORMALIZATION_KEY]):
+        case RowNormalization.NORMUON:
+            rowd = _workspace.buffer(device, "rowd", (blocks, k), torch.float32)
+            scratch = _workspace.buffer(device, "row_scratch", (2 * blocks * k,), torch.float32)
+            scale = _workspace.buffer(device, "scale", (blocks,), torch.float32)
+            _lib.call("dionw_normuon_stats", orthogonal.data_ptr(), blocks, k, rows, cols,
+                      idx_ptr, run.variance.data_ptr(), float(group[MUON_BETA2_KEY]), step,
+                      rowd.data_ptr(), scratch.data_ptr(), scale.data_ptr(), stream)
+        case RowNormalization.NONE:
+            pass
+        case _ as unreachable:
+            raise RuntimeError(f"Unhandled RowNormalization: {unreachable}")
+
+    weight_decay = float(group["weight_decay"])
+    decay = 1.0 - lr * weight_decay
+    _lib.call("dionw_apply_update", _lib.ptr_array(run.params), count, per_param, rows, cols, k,
+              orthogonal.data_ptr(), idx_ptr, None if slot is None else slot.data_ptr(),
+              None if rowd is None else rowd.data_ptr(),
+              None if scale is None else scale.data_ptr(), step, decay,
+              int(weight_decay > 0.0), stream)
+    for param, copy in run.writeback:
+        param.copy_(copy)

@@ -1,0 +1,601 @@
+// MFMA products of the Newton-Schulz iterations and their drivers.
+//
+// Every product is one "NT" form, C[i,j] = sum_k A[i,k] B[j,k] with both
+// operands row-major along k, computed with v_mfma_f32_32x32x16_{f16,bf16}
+// (fp32 accumulation) from LDS-staged 64-deep k tiles. The epilogue forms
+// alpha * acc + beta * D[i,j] and rounds once to the storage type.
+//
+//  symmetric mode  only tiles on and above the diagonal are computed and each
+//                  is stored twice (itself and its mirror): X X^T (syrk,
+//                  _symmetric_kernels.py:81-144), c A A + b A of a symmetric A
+//                  (:147-218), and the products of the commuting symmetric
+//                  polynomials in X X^T that Gram Newton-Schulz updates
+//                  (_gram.py:58-69).
+//  transposed out  a second store of C^T, so that the next product can read
+//                  the result as its B operand (B must be k-contiguous).
+//
+// Drivers: dionw_newton_schulz sequences the Gram iteration (_gram.py:50-69,
+// restart at iteration 2), the standard Polar Express iteration for square
+// blocks (_gram.py:41-47) and the bf16 quintic of Keller / Polar Express
+// (_polar_express.py:74-104) over a caller-provided workspace.
+#include "common.h"
+
+#include <cmath>
+#include <mutex>
+
+namespace dionw {
+namespace {
+
+constexpr int BK = 64;  // k depth of one LDS stage (4 MFMA k-steps of 16)
+
+enum OutMode : int { kOutSame = 0, kOutBf16ViaF16 = 1 };
+
+struct GemmArgs {
+  const void* a;
+  const void* b;
+  const void* d;
+  void* c;
+  void* ct;
+  void* c_diag;
+  int64_t lda, ldb, ldd, ldc, ldct;
+  int64_t sa, sb, sd, sc, sct;
+  int m, n, k;          // compute extents
+  int m_lim, n_lim;     // store extents (<= m, n)
+  float alpha, beta, diag_shift;
+  int sym;
+  int ct_vec;           // transposed store may use 8-byte vectors
+  int tiles_m, tiles_n;
+};
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<_Float16> {
+  typedef f16x8 vec;
+  __device__ static f32x16 run(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<__bf16> {
+  typedef bf16x8 vec;
+  __device__ static f32x16 run(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// LDS layout of a [rows][64] k tile: 16-byte chunk q of row r sits at chunk
+// q ^ ((r >> 1) & 7), so the 16 lanes of a read phase (rows r..r+15, same
+// chunk) land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * BK + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
+
+template <typename OUT_T, int MODE>
+__device__ __forceinline__ OUT_T round_out(float v) {
+  if (MODE == kOutBf16ViaF16) return (OUT_T)(float)(_Float16)v;
+  return (OUT_T)v;
+}
+
+// Decodes the upper-triangle tile t (0 .. T(T+1)/2 - 1) into (tm, tn), tm <= tn.
+__device__ __forceinline__ void tri_tile(int t, int& tm, int& tn) {
+  int n = (int)((sqrtf(8.f * (float)t + 1.f) - 1.f) * 0.5f);
+  while ((n + 1) * (n + 2) / 2 <= t) ++n;
+  while (n * (n + 1) / 2 > t) --n;
+  tn = n;
+  tm = t - n * (n + 1) / 2;
+}
+
+template <typename T, typename OUT_T, int BM, int BN, int WM, int WN, int MODE>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmArgs g) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 fragments per wave
+  constexpr int A_CH = BM * BK / 8 / NT;        // 16-byte chunks per thread
+  constexpr int B_CH = BN * BK / 8 / NT;
+  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for the thread count");
+  using V = typename Mfma<T>::vec;
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  T* lds = reinterpret_cast<T*>(smem);
+  constexpr int STAGE = (BM + BN) * BK;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int64_t batch = blockIdx.y;
+
+  int tm, tn;
+  if (g.sym) {
+    tri_tile(blockIdx.x, tm, tn);
+  } else {
+    // Groups of 8 tile rows sweep the columns together (operand reuse in L2).
+    const int t = blockIdx.x;
+    const int group = 8 * g.tiles_n;
+    const int first = (t / group) * 8;
+    const int gm = min(g.tiles_m - first, 8);
+    tm = first + (t % group) % gm;
+    tn = (t % group) / gm;
+  }
+  const int m0 = tm * BM, n0 = tn * BN;
+  const T* A = reinterpret_cast<const T*>(g.a) + batch * g.sa;
+  const T* B = reinterpret_cast<const T*>(g.b) + batch * g.sb;
+
+  u32x4 ra[A_CH], rb[B_CH];
+  auto load = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int c = 0; c < A_CH; ++c) {
+      const int q = tid + c * NT;
+      const int row = q >> 3, ch = q & 7;
+      const int gr = m0 + row, gk = k0 + ch * 8;
+      ra[c] = (gr < g.m && gk < g.k)
+                  ? *reinterpret_cast<const u32x4*>(A + (int64_t)gr * g.lda + gk)
+                  : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int c = 0; c < B_CH; ++c) {
+      const int q = tid + c * NT;
+      const int row = q >> 3, ch = q & 7;
+      const int gr = n0 + row, gk = k0 + ch * 8;
+      rb[c] = (gr < g.n && gk < g.k)
+                  ? *reinterpret_cast<const u32x4*>(B + (int64_t)gr * g.ldb + gk)
+                  : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int buf) {
+    T* As = lds + buf * STAGE;
+    T* Bs = As + BM * BK;
+#pragma unroll
+    for (int c = 0; c < A_CH; ++c) {
+      const int q = tid + c * NT;
+      *reinterpret_cast<u32x4*>(As + lds_off(q >> 3, q & 7)) = ra[c];
+    }
+#pragma unroll
+    for (int c = 0; c < B_CH; ++c) {
+      const int q = tid + c * NT;
+      *reinterpret_cast<u32x4*>(Bs + lds_off(q >> 3, q & 7)) = rb[c];
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int kt_count = (g.k + BK - 1) / BK;
+  load(0);
+  store(0);
+  __syncthreads();
+  const int lrow = lane & 31, lk = lane >> 5;
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < kt_count) load(kt + 1);
+    const T* As = lds + buf * STAGE;
+    const T* Bs = As + BM * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      V af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const V*>(As + lds_off(wm * WTM + i * 32 + lrow, 2 * ks + lk));
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const V*>(Bs + lds_off(wn * WTN + j * 32 + lrow, 2 * ks + lk));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<T>::run(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < kt_count) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue. Fragment element e of lane l holds row 8(e/4) + 4(l/32) + e%4,
+  // column l%32 of its 32x32 block.
+  const T* D = g.d ? reinterpret_cast<const T*>(g.d) + batch * g.sd : nullptr;
+  OUT_T* C = g.c ? reinterpret_cast<OUT_T*>(g.c) + batch * g.sc : nullptr;
+  OUT_T* CT = g.ct ? reinterpret_cast<OUT_T*>(g.ct) + batch * g.sct : nullptr;
+  OUT_T* CD = g.c_diag ? reinterpret_cast<OUT_T*>(g.c_diag) + batch * g.sc : nullptr;
+  const bool diag_tile = g.sym && tm == tn;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + wn * WTN + j * 32 + lrow;
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int row0 = m0 + wm * WTM + i * 32 + 8 * e4 + 4 * lk;
+        OUT_T v[4], vd[4];
+        bool in[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = row0 + e;
+          in[e] = row < g.m_lim && col < g.n_lim;
+          float x = g.alpha * acc[i][j][4 * e4 + e];
+          if (D && in[e]) x += g.beta * (float)D[(int64_t)row * g.ldd + col];
+          v[e] = round_out<OUT_T, MODE>(x);
+          if (CD) {
+            float y = (float)v[e] + (row == col ? g.diag_shift : 0.f);
+            vd[e] = (OUT_T)y;
+          }
+        }
+        // Straight store: on the diagonal tile only the upper half (i <= j).
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = row0 + e;
+          if (!in[e] || (diag_tile && row > col)) continue;
+          if (C) C[(int64_t)row * g.ldc + col] = v[e];
+          if (CD) CD[(int64_t)row * g.ldc + col] = vd[e];
+        }
+        // Transposed / mirrored store: 4 consecutive rows -> one 8-byte store.
+        if (CT || (g.sym && CD)) {
+          const bool full4 = g.ct_vec && in[0] && in[3] && !(diag_tile && row0 + 3 >= col);
+          if (full4 && CT) {
+            typedef OUT_T o4 __attribute__((ext_vector_type(4)));
+            o4 w = {v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<o4*>(CT + (int64_t)col * g.ldct + row0) = w;
+            if (g.sym && CD) {
+              o4 wd = {vd[0], vd[1], vd[2], vd[3]};
+              *reinterpret_cast<o4*>(CD + (int64_t)col * g.ldc + row0) = wd;
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int row = row0 + e;
+              if (!in[e] || (diag_tile && row >= col)) continue;
+              if (CT) CT[(int64_t)col * g.ldct + row] = v[e];
+              if (g.sym && CD) CD[(int64_t)col * g.ldc + row] = vd[e];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---- launch configuration ----------------------------------------------------
+
+struct Problem {
+  int elem;  // kF16 / kBF16
+  int out_mode;
+  int64_t batch;
+  GemmArgs g;
+};
+
+template <typename T, typename OUT_T, int BM, int BN, int WM, int WN, int MODE>
+int launch_cfg(const Problem& p, hipStream_t stream) {
+  GemmArgs g = p.g;
+  g.ct_vec = !g.ct || (g.ldct % 4 == 0 && g.sct % 4 == 0 &&
+                       (reinterpret_cast<uintptr_t>(g.ct) & 7) == 0);
+  if (g.c_diag && g.sym) g.ct_vec = g.ct_vec && g.ldc % 4 == 0 && g.sc % 4 == 0;
+  constexpr size_t lds_bytes = 2 * (size_t)(BM + BN) * BK * sizeof(T);
+  auto kern = gemm_nt_kernel<T, OUT_T, BM, BN, WM, WN, MODE>;
+  static std::once_flag once;
+  static hipError_t attr_rc = hipSuccess;
+  std::call_once(once, [&] {
+    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+  });
+  if (attr_rc != hipSuccess) {
+    set_error("gemm: hipFuncSetAttribute failed: %s", hipGetErrorString(attr_rc));
+    return kHipError;
+  }
+  g.tiles_m = (g.m + BM - 1) / BM;
+  g.tiles_n = (g.n + BN - 1) / BN;
+  int64_t tiles;
+  if (g.sym) {
+    if (BM != BN || g.m != g.n) {
+      set_error("gemm: symmetric mode needs a square output and square tiles");
+      return kInvalid;
+    }
+    tiles = (int64_t)g.tiles_m * (g.tiles_m + 1) / 2;
+  } else {
+    tiles = (int64_t)g.tiles_m * g.tiles_n;
+  }
+  if (tiles > INT32_MAX || p.batch > 65535) {
+    set_error("gemm: grid too large");
+    return kInvalid;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)p.batch), dim3(WM * WN * 64),
+                     lds_bytes, stream, g);
+  return check_launch("gemm_nt");
+}
+
+template <typename T, typename OUT_T, int MODE>
+int launch_typed(const Problem& p, hipStream_t stream) {
+  // Large outputs: 128x128 tiles (4 waves of 64x64); small ones 64x64 tiles
+  // so that a batch of small blocks still fills the 256 CUs.
+  const int64_t big_tiles = p.batch * ((p.g.m + 127) / 128) * ((p.g.n + 127) / 128) /
+                            (p.g.sym ? 2 : 1);
+  if (big_tiles >= 512) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
+  return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
+}
+
+int launch(const Problem& p, hipStream_t stream) {
+  const GemmArgs& g = p.g;
+  if (g.m <= 0 || g.n <= 0 || g.k <= 0 || p.batch <= 0) return kOk;
+  if (g.k % 8 || g.lda % 8 || g.ldb % 8 || g.sa % 8 || g.sb % 8 ||
+      !aligned16(g.a) || !aligned16(g.b)) {
+    set_error("gemm: k, operand row strides and batch strides must be multiples of 8 "
+              "elements and operands 16-byte aligned");
+    return kInvalid;
+  }
+  if (p.elem == kF16) {
+    if (p.out_mode == kOutBf16ViaF16) return launch_typed<_Float16, __bf16, kOutBf16ViaF16>(p, stream);
+    return launch_typed<_Float16, _Float16, kOutSame>(p, stream);
+  }
+  if (p.elem == kBF16) return launch_typed<__bf16, __bf16, kOutSame>(p, stream);
+  set_error("gemm: unsupported element type %d", p.elem);
+  return kInvalid;
+}
+
+// ---- Newton-Schulz drivers ---------------------------------------------------
+
+struct Mat {  // a batch of row-major matrices
+  void* p;
+  int64_t ld, stride;
+};
+
+Problem product(int elem, int64_t batch, int m, int n, int k, Mat a, Mat b) {
+  Problem p{};
+  p.elem = elem;
+  p.out_mode = kOutSame;
+  p.batch = batch;
+  p.g.a = a.p;
+  p.g.lda = a.ld;
+  p.g.sa = a.stride;
+  p.g.b = b.p;
+  p.g.ldb = b.ld;
+  p.g.sb = b.stride;
+  p.g.m = p.g.m_lim = m;
+  p.g.n = p.g.n_lim = n;
+  p.g.k = k;
+  p.g.alpha = 1.f;
+  p.g.beta = 0.f;
+  return p;
+}
+
+void set_out(Problem& p, Mat c) {
+  p.g.c = c.p;
+  p.g.ldc = c.ld;
+  p.g.sc = c.stride;
+}
+void set_out_t(Problem& p, Mat ct) {
+  p.g.ct = ct.p;
+  p.g.ldct = ct.ld;
+  p.g.sct = ct.stride;
+}
+void set_addend(Problem& p, Mat d, float alpha, float beta) {
+  p.g.d = d.p;
+  p.g.ldd = d.ld;
+  p.g.sd = d.stride;
+  p.g.alpha = alpha;
+  p.g.beta = beta;
+}
+void make_symmetric(Problem& p) {
+  p.g.sym = 1;
+  p.g.ct = p.g.c;
+  p.g.ldct = p.g.ldc;
+  p.g.sct = p.g.sc;
+}
+
+// Polar Express coefficients of the Gram iteration: the 5 published rows with
+// the 1.05 safety factor folded in as (a / s, b / s^3, c / s^5).
+void gram_coefficients(double out[5][3]) {
+  static const double raw[5][3] = {
+      {8.28721201814563, -23.595886519098837, 17.300387312530933},
+      {4.107059111542203, -2.9478499167379106, 0.5448431082926601},
+      {3.9486908534822946, -2.908902115962949, 0.5518191394370137},
+      {3.3184196573706015, -2.488488024314874, 0.51004894012372},
+      {2.300652019954817, -1.6689039845747493, 0.4188073119525673},
+  };
+  const double s = 1.05;
+  for (int i = 0; i < 5; ++i) {
+    out[i][0] = raw[i][0] / s;
+    out[i][1] = raw[i][1] / (s * s * s);
+    out[i][2] = raw[i][2] / (s * s * s * s * s);
+  }
+}
+
+void polar_express_coefficients(double out[5][3]) {
+  static const double pe[5][3] = {
+      {8.156554524902461, -22.48329292557795, 15.878769915207462},
+      {4.042929935166739, -2.808917465908714, 0.5000178451051316},
+      {3.8916678022926607, -2.772484153217685, 0.5060648178503393},
+      {3.285753657755655, -2.3681294933425376, 0.46449024233003106},
+      {2.3465413258596377, -1.7097828382687081, 0.42323551169305323},
+  };
+  for (int i = 0; i < 5; ++i)
+    for (int j = 0; j < 3; ++j) out[i][j] = pe[i][j];
+}
+
+void keller_coefficients(double out[5][3]) {
+  for (int i = 0; i < 5; ++i) {
+    out[i][0] = 3.4445;
+    out[i][1] = -4.7750;
+    out[i][2] = 2.0315;
+  }
+}
+
+enum Kind : int { kGram = 0, kPolarExpress = 1, kKeller = 2 };
+
+size_t elems_needed(int kind, int64_t batch, int64_t r, int64_t c) {
+  const bool gram = kind == kGram;  // the Gram iteration needs the most
+  const int64_t sq = r * r, rc = r * c;
+  return (size_t)batch * (gram ? (6 * sq + rc) : (2 * sq + rc));
+}
+
+// Final store of the real region into the bf16 output (W orientation).
+void set_final_out(Problem& p, void* out, int transposed, int64_t out_ld, int64_t out_stride,
+                   int64_t m_real, int64_t n_real) {
+  p.g.m_lim = (int)m_real;
+  p.g.n_lim = (int)n_real;
+  if (transposed)
+    set_out_t(p, Mat{out, out_ld, out_stride});
+  else
+    set_out(p, Mat{out, out_ld, out_stride});
+}
+
+}  // namespace
+}  // namespace dionw
+
+using namespace dionw;
+
+extern "C" {
+
+int dionw_gemm_nt(int32_t elem, int64_t batch, int64_t m, int64_t n, int64_t k, const void* a,
+                  int64_t lda, int64_t stride_a, const void* b, int64_t ldb, int64_t stride_b,
+                  const void* d, int64_t ldd, int64_t stride_d, float alpha, float beta, void* c,
+                  int64_t ldc, int64_t stride_c, void* ct, int64_t ldct, int64_t stride_ct,
+                  int32_t symmetric, hipStream_t stream) {
+  DIONW_REQUIRE(a && b && (c || ct), "gemm_nt: null operand");
+  DIONW_REQUIRE(m > 0 && n > 0 && k > 0 && m < INT32_MAX && n < INT32_MAX && k < INT32_MAX,
+                "gemm_nt: bad sizes");
+  DIONW_REQUIRE(!symmetric || (m == n && c && !ct), "gemm_nt: symmetric output needs m == n "
+                "and a single output");
+  Problem p = product(elem, batch, (int)m, (int)n, (int)k, Mat{(void*)a, lda, stride_a},
+                      Mat{(void*)b, ldb, stride_b});
+  if (d) set_addend(p, Mat{(void*)d, ldd, stride_d}, alpha, beta);
+  else p.g.alpha = alpha;
+  if (c) set_out(p, Mat{c, ldc, stride_c});
+  if (ct) set_out_t(p, Mat{ct, ldct, stride_ct});
+  if (symmetric) make_symmetric(p);
+  return launch(p, stream);
+}
+
+size_t dionw_newton_schulz_workspace(int32_t kind, int64_t batch, int64_t r, int64_t c) {
+  return elems_needed(kind, batch, r, c) * 2;
+}
+
+int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void* xt,
+                        int64_t r_real, int64_t c_real, void* out, int32_t out_transposed,
+                        int64_t out_ld, int64_t out_stride, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  DIONW_REQUIRE(kind == kGram || kind == kPolarExpress || kind == kKeller,
+                "newton_schulz: unknown kind %d", kind);
+  DIONW_REQUIRE(x && xt && out && workspace, "newton_schulz: null pointer");
+  DIONW_REQUIRE(r > 0 && c >= r && r % 8 == 0 && c % 8 == 0 && r < 65536 && c < INT32_MAX,
+                "newton_schulz: need 0 < r <= c, both multiples of 8 (r=%lld c=%lld)",
+                (long long)r, (long long)c);
+  DIONW_REQUIRE(r_real <= r && c_real <= c && r_real > 0 && c_real > 0,
+                "newton_schulz: real extents exceed the padded ones");
+  DIONW_REQUIRE(workspace_bytes >= dionw_newton_schulz_workspace(kind, batch, r, c),
+                "newton_schulz: workspace too small");
+  if (batch == 0) return kOk;
+  const int R = (int)r, C = (int)c;
+  const int64_t sq = r * r, rc = r * c;
+  const int elem = kind == kGram ? kF16 : kBF16;
+  auto* ws = reinterpret_cast<uint16_t*>(workspace);
+  auto mat_sq = [&](int slot) { return Mat{ws + (size_t)slot * batch * sq, r, sq}; };
+  Mat X{x, c, rc}, XT{xt, r, rc};
+  double coef[5][3];
+
+  if (kind == kGram && c_real > r_real) {
+    gram_coefficients(coef);
+    Mat G = mat_sq(0), G2 = mat_sq(1), Z = mat_sq(2), Q = mat_sq(3), Q2 = mat_sq(4),
+        RZ = mat_sq(5);
+    Mat XT2{ws + (size_t)6 * batch * sq, r, rc};
+    // G = X X^T
+    Problem p = product(elem, batch, R, R, C, X, X);
+    set_out(p, G);
+    make_symmetric(p);
+    DIONW_TRY(launch(p, stream));
+    Mat xt_cur = XT;
+    for (int i = 0; i < 5; ++i) {
+      const float a = (float)coef[i][0], bb = (float)coef[i][1], cc = (float)coef[i][2];
+      if (i == 2) {
+        // Restart: X = Q X (in place on X; its transpose goes to XT2), G = X X^T.
+        p = product(elem, batch, R, C, R, Q, xt_cur);
+        set_out(p, X);
+        set_out_t(p, XT2);
+        DIONW_TRY(launch(p, stream));
+        xt_cur = XT2;
+        p = product(elem, batch, R, R, C, X, X);
+        set_out(p, G);
+        make_symmetric(p);
+        DIONW_TRY(launch(p, stream));
+      }
+      // Z = c G G + b G; at iterations 0 and 2 also Q = Z + a I.
+      p = product(elem, batch, R, R, R, G, G);
+      set_addend(p, G, cc, bb);
+      set_out(p, Z);
+      make_symmetric(p);
+      if (i == 0 || i == 2) {
+        p.g.c_diag = Q.p;
+        p.g.diag_shift = a;
+      }
+      DIONW_TRY(launch(p, stream));
+      if (i != 0 && i != 2) {
+        // Q = a Q + Q Z
+        p = product(elem, batch, R, R, R, Q, Z);
+        set_addend(p, Q, 1.f, a);
+        set_out(p, Q2);
+        make_symmetric(p);
+        DIONW_TRY(launch(p, stream));
+        std::swap(Q, Q2);
+      }
+      if (i < 4 && i + 1 != 2) {
+        // RZ = a G + G Z; G = a RZ + Z RZ
+        p = product(elem, batch, R, R, R, G, Z);
+        set_addend(p, G, 1.f, a);
+        set_out(p, RZ);
+        make_symmetric(p);
+        DIONW_TRY(launch(p, stream));
+        p = product(elem, batch, R, R, R, Z, RZ);
+        set_addend(p, RZ, 1.f, a);
+        set_out(p, G2);
+        make_symmetric(p);
+        DIONW_TRY(launch(p, stream));
+        std::swap(G, G2);
+      }
+    }
+    // out = Q X, rounded to fp16 then bf16.
+    p = product(elem, batch, R, C, R, Q, xt_cur);
+    p.out_mode = kOutBf16ViaF16;
+    set_final_out(p, out, out_transposed, out_ld, out_stride, r_real, c_real);
+    return launch(p, stream);
+  }
+
+  // Standard iteration (square Gram blocks, fp16) or the bf16 quintic:
+  // X = a X + (c A A + b A) X with A = X X^T, five times.
+  if (kind == kGram) gram_coefficients(coef);
+  else if (kind == kPolarExpress) polar_express_coefficients(coef);
+  else keller_coefficients(coef);
+  Mat G = mat_sq(0), P = mat_sq(1);
+  Mat XT2{ws + (size_t)2 * batch * sq, r, rc};
+  Mat xt_cur = XT, xt_next = XT2;
+  for (int i = 0; i < 5; ++i) {
+    const float a = (float)coef[i][0], bb = (float)coef[i][1], cc = (float)coef[i][2];
+    Problem p = product(elem, batch, R, R, C, X, X);
+    set_out(p, G);
+    make_symmetric(p);
+    DIONW_TRY(launch(p, stream));
+    p = product(elem, batch, R, R, R, G, G);
+    set_addend(p, G, cc, bb);
+    set_out(p, P);
+    make_symmetric(p);
+    DIONW_TRY(launch(p, stream));
+    p = product(elem, batch, R, C, R, P, xt_cur);
+    set_addend(p, X, 1.f, a);
+    if (i < 4) {
+      set_out(p, X);  // X is only read as the addend, element by element
+      set_out_t(p, xt_next);
+      DIONW_TRY(launch(p, stream));
+      std::swap(xt_cur, xt_next);
+    } else {
+      if (kind == kGram) p.out_mode = kOutBf16ViaF16;
+      set_final_out(p, out, out_transposed, out_ld, out_stride, r_real, c_real);
+      DIONW_TRY(launch(p, stream));
+    }
+  }
+  return kOk;
+}
+
+}  // extern "C"

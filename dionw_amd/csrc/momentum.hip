@@ -1,0 +1,429 @@
+// Momentum passes of a Dion bucket run and the Newton-Schulz input cast.
+//
+//  accumulate   M += G per row, with the row's l1 score and sum of squares
+//               (the selected path; replaces _momentum_kernels.py:40-55).
+//  full sumsq   sum of squares of the Newton-Schulz input U of every row, no
+//               writes (first pass of the every-row path, _momentum_kernels.py:58-77).
+//  block denom  per block: sqrt(sum of the rows' sums of squares) + eps.
+//  prepare      the single pass that writes the decayed momentum and the
+//               normalized 16-bit Newton-Schulz input in both orientations
+//               (_matrix_step.py:172-178 and _gram.py:83-87 fused).
+//
+// Row reductions use one wavefront per row. A lane accumulates four partial
+// sums (one per float4 component) over its float4 chunks in column order,
+// combines them as (x + y) + (z + w), then the lanes combine by the xor
+// butterfly of wave_sum: the l1 score is a fixed-order fp32 sum that the CPU
+// oracle restates bit for bit.
+#pragma clang fp contract(off)
+
+#include "common.h"
+
+#include <type_traits>
+
+namespace dionw {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // 4 wavefronts of 256 threads, one row each
+
+enum AccMode : int { kScores = 0, kFullSumsq = 1 };
+
+struct AccArgs {
+  RowTable t;
+  float* momentum;        // [count * rows_per_tensor, cols], run-contiguous
+  float* scores;          // [rows] l1 of M + G (kScores)
+  float* rowsq;           // [rows] sum of squares of M + G, or of U (kFullSumsq)
+  int64_t rows_per_tensor;
+  int64_t cols;
+  float mu;               // kFullSumsq: momentum decay
+  int nesterov;           // kFullSumsq: U = G + mu (M + G) instead of M + G
+  int vec;                // float4 path: cols % 4 == 0 and 16-byte aligned rows
+};
+
+template <int MODE>
+__global__ __launch_bounds__(256) void accumulate_kernel(AccArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int64_t total = (int64_t)a.t.count * a.rows_per_tensor;
+  if (row >= total) return;
+  const int tensor = (int)(row / a.rows_per_tensor);
+  const int64_t local = row - (int64_t)tensor * a.rows_per_tensor;
+  const float* g = a.t.grad[tensor] + local * a.cols;
+  float* m = a.momentum ? a.momentum + row * a.cols : nullptr;
+
+  f32x4 l1 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 sq = {0.f, 0.f, 0.f, 0.f};
+  if (a.vec) {
+    const int64_t n4 = a.cols >> 2;
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
+    f32x4* m4 = reinterpret_cast<f32x4*>(m);
+    for (int64_t c = lane; c < n4; c += kWave) {
+      f32x4 gv = __builtin_nontemporal_load(g4 + c);
+      f32x4 mv = (MODE == kScores || a.momentum) ? m4[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 s = mv + gv;
+      if (MODE == kScores) {
+        m4[c] = s;
+        l1 += __builtin_elementwise_abs(s);
+        sq += s * s;
+      } else {
+        f32x4 u = s;
+        if (a.nesterov) u = gv + s * a.mu;
+        sq += u * u;
+      }
+    }
+  } else {
+    // Scalar path (any cols, any alignment): component 0 carries the sums.
+    for (int64_t c = lane; c < a.cols; c += kWave) {
+      float gv = g[c];
+      float s = ((MODE == kScores || a.momentum) ? m[c] : 0.f) + gv;
+      if (MODE == kScores) {
+        m[c] = s;
+        l1.x += fabsf(s);
+        sq.x += s * s;
+      } else {
+        float u = a.nesterov ? gv + s * a.mu : s;
+        sq.x += u * u;
+      }
+    }
+  }
+  float sqs = wave_sum((sq.x + sq.y) + (sq.z + sq.w));
+  if (MODE == kScores) {
+    float l = wave_sum((l1.x + l1.y) + (l1.z + l1.w));
+    if (lane == 0) {
+      a.scores[row] = l;
+      a.rowsq[row] = sqs;
+    }
+  } else if (lane == 0) {
+    a.rowsq[row] = sqs;
+  }
+}
+
+// den[b] = sqrt(sum of rowsq over the block's rows) * safety + eps; one wave per block.
+__global__ __launch_bounds__(64) void block_denom_kernel(const float* rowsq, float* den,
+                                                         int64_t rows, float safety, float eps) {
+  const int64_t b = blockIdx.x;
+  const float* r = rowsq + b * rows;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < rows; i += kWave) s += r[i];
+  s = wave_sum(s);
+  if (threadIdx.x == 0) den[b] = sqrtf(s) * safety + eps;
+}
+
+// ---- prepare: decayed momentum + normalized 16-bit Newton-Schulz input ------
+
+struct PrepArgs {
+  RowTable t;             // gradients (full mode only)
+  float* momentum;        // run momentum [B, rows, cols]
+  const int32_t* idx;     // [B, k] selected rows (ascending), nullptr in full mode
+  const float* den;       // [B] Frobenius norm + eps of the block's input
+  void* out_r;            // [B, P_pad, J_pad]: row p of the input, W orientation
+  void* out_t;            // [B, J_pad, P_pad]: its transpose (may be nullptr)
+  int64_t rows, cols, k;  // block rows, cols, selected rows
+  int64_t p_pad, j_pad;   // padded extents (zeros written in the padding)
+  int64_t blocks_per_tensor;
+  float mu;
+  int full;               // every row: M = mu (M + G), U = M + G or Nesterov
+  int nesterov;
+  int write_m;            // write the decayed momentum
+  int elem;               // kF16, kBF16 (quintic: bf16 input rounded first), kF32 (raw)
+  int vec;                // float4 loads are legal (cols % 4 == 0, aligned)
+};
+
+constexpr int kTile = 64;
+
+template <int ELEM>
+__global__ __launch_bounds__(256) void prepare_kernel(PrepArgs a) {
+  using T = typename std::conditional<ELEM == kF16, _Float16, __bf16>::type;
+  __shared__ T tile[kTile][kTile + 8];
+  const int tx = threadIdx.x & 15;   // 4 columns each
+  const int ty = threadIdx.x >> 4;   // rows ty + 16 i
+  const int64_t b = blockIdx.z;
+  const int64_t j0 = (int64_t)blockIdx.x * kTile + 4 * tx;
+  const int64_t p_base = (int64_t)blockIdx.y * kTile;
+  const float den = a.den[b];
+
+  T vals[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t p = p_base + ty + 16 * i;
+    float u[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p < a.k) {
+      const int64_t src_row = a.full ? p : (int64_t)a.idx[b * a.k + p];
+      float* m = a.momentum ? a.momentum + (b * a.rows + src_row) * a.cols : nullptr;
+      const float* g = nullptr;
+      if (a.full) {
+        const int64_t tensor = b / a.blocks_per_tensor;
+        const int64_t local_row = (b - tensor * a.blocks_per_tensor) * a.rows + p;
+        g = a.t.grad[tensor] + local_row * a.cols;
+      }
+      if (a.vec && j0 + 3 < a.cols) {
+        f32x4 mv = m ? *reinterpret_cast<const f32x4*>(m + j0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 uv, nm;
+        if (a.full) {
+          f32x4 gv = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g + j0));
+          f32x4 s = mv + gv;
+          nm = s * a.mu;
+          uv = a.nesterov ? gv + nm : s;
+        } else {
+          uv = mv;
+          nm = mv * a.mu;
+        }
+        if (a.write_m) *reinterpret_cast<f32x4*>(m + j0) = nm;
+        u[0] = uv.x; u[1] = uv.y; u[2] = uv.z; u[3] = uv.w;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int64_t j = j0 + c;
+          if (j < a.cols) {
+            float mv = m ? m[j] : 0.f, uv, nm;
+            if (a.full) {
+              float gv = g[j];
+              float s = mv + gv;
+              nm = s * a.mu;
+              uv = a.nesterov ? gv + nm : s;
+            } else {
+              uv = mv;
+              nm = mv * a.mu;
+            }
+            if (a.write_m) m[j] = nm;
+            u[c] = uv;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float x;
+      if (ELEM == kBF16) {
+        // Keller / Polar Express: the input is rounded to bf16 before the division.
+        x = (float)(__bf16)u[c] / den;
+      } else {
+        x = u[c] / den;
+      }
+      vals[i][c] = (T)x;  // padding rows/cols hold u = 0 -> 0
+    }
+  }
+  // Row-major output [P_pad, J_pad].
+  T* out_r = reinterpret_cast<T*>(a.out_r) + b * a.p_pad * a.j_pad;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t p = p_base + ty + 16 * i;
+    if (p < a.p_pad) {
+      if (j0 + 3 < a.j_pad) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 v = {vals[i][0], vals[i][1], vals[i][2], vals[i][3]};
+        *reinterpret_cast<t4*>(out_r + p * a.j_pad + j0) = v;
+      } else {
+        for (int c = 0; c < 4; ++c)
+          if (j0 + c < a.j_pad) out_r[p * a.j_pad + j0 + c] = vals[i][c];
+      }
+    }
+  }
+  if (a.out_t == nullptr) return;
+  // Transposed output [J_pad, P_pad] through LDS.
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) tile[4 * tx + c][ty + 16 * i] = vals[i][c];
+  __syncthreads();
+  T* out_t = reinterpret_cast<T*>(a.out_t) + b * a.j_pad * a.p_pad;
+  const int jj = threadIdx.x >> 2;          // tile column -> output row
+  const int pp = (threadIdx.x & 3) * 16;    // 16 consecutive p
+  const int64_t j = (int64_t)blockIdx.x * kTile + jj;
+  if (j < a.j_pad) {
+    T* dst = out_t + j * a.p_pad + p_base + pp;
+    if (p_base + pp + 15 < a.p_pad) {
+      typedef T t8 __attribute__((ext_vector_type(8)));
+      t8 v0, v1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v0[e] = tile[jj][pp + e];
+        v1[e] = tile[jj][pp + 8 + e];
+      }
+      reinterpret_cast<t8*>(dst)[0] = v0;
+      reinterpret_cast<t8*>(dst)[1] = v1;
+    } else {
+      for (int e = 0; e < 16; ++e)
+        if (p_base + pp + e < a.p_pad) dst[e] = tile[jj][pp + e];
+    }
+  }
+}
+
+// Raw fp32 copy of the input rows for a user-supplied orthogonalization
+// ([B, k, cols], no normalization), with the same momentum writes.
+__global__ __launch_bounds__(256) void prepare_raw_kernel(PrepArgs a) {
+  const int64_t b = blockIdx.z;
+  const int64_t p = (int64_t)blockIdx.y;
+  float* out = reinterpret_cast<float*>(a.out_r) + (b * a.k + p) * a.cols;
+  const int64_t src_row = a.full ? p : (int64_t)a.idx[b * a.k + p];
+  float* m = a.momentum ? a.momentum + (b * a.rows + src_row) * a.cols : nullptr;
+  const float* g = nullptr;
+  if (a.full) {
+    const int64_t tensor = b / a.blocks_per_tensor;
+    const int64_t local_row = (b - tensor * a.blocks_per_tensor) * a.rows + p;
+    g = a.t.grad[tensor] + local_row * a.cols;
+  }
+  for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < a.cols;
+       j += (int64_t)gridDim.x * 256) {
+    float mv = m ? m[j] : 0.f, uv, nm;
+    if (a.full) {
+      float gv = g[j];
+      float s = mv + gv;
+      nm = s * a.mu;
+      uv = a.nesterov ? gv + nm : s;
+    } else {
+      uv = mv;
+      nm = mv * a.mu;
+    }
+    if (a.write_m) m[j] = nm;
+    out[j] = uv;
+  }
+}
+
+bool table_aligned(const RowTable& t, int64_t cols) {
+  if (cols % 4) return false;
+  for (int i = 0; i < t.count; ++i)
+    if (!aligned16(t.grad[i])) return false;
+  return true;
+}
+
+}  // namespace
+}  // namespace dionw
+
+using namespace dionw;
+
+extern "C" {
+
+int dionw_accumulate_scores(const float* const* grads, int32_t count, int64_t rows_per_tensor,
+                            int64_t cols, float* momentum, float* scores, float* row_sumsq,
+                            hipStream_t stream) {
+  DIONW_REQUIRE(count >= 0 && rows_per_tensor > 0 && cols > 0,
+                "accumulate_scores: bad sizes (count=%d rows=%lld cols=%lld)", count,
+                (long long)rows_per_tensor, (long long)cols);
+  DIONW_REQUIRE(momentum && scores && row_sumsq, "accumulate_scores: null output");
+  for (int32_t start = 0; start < count; start += kMaxTensors) {
+    AccArgs a{};
+    a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
+    for (int i = 0; i < a.t.count; ++i) {
+      DIONW_REQUIRE(grads[start + i], "accumulate_scores: null gradient %d", start + i);
+      a.t.grad[i] = grads[start + i];
+    }
+    const int64_t row0 = (int64_t)start * rows_per_tensor;
+    a.momentum = momentum + row0 * cols;
+    a.scores = scores + row0;
+    a.rowsq = row_sumsq + row0;
+    a.rows_per_tensor = rows_per_tensor;
+    a.cols = cols;
+    a.vec = table_aligned(a.t, cols) && aligned16(a.momentum);
+    const int64_t rows = (int64_t)a.t.count * rows_per_tensor;
+    hipLaunchKernelGGL(accumulate_kernel<kScores>, dim3((unsigned)ceil_div(rows, kRowsPerBlock)),
+                       dim3(256), 0, stream, a);
+    DIONW_TRY(check_launch("accumulate_scores"));
+  }
+  return kOk;
+}
+
+int dionw_full_sumsq(const float* const* grads, int32_t count, int64_t rows_per_tensor,
+                     int64_t cols, const float* momentum, float mu, int32_t nesterov,
+                     float* row_sumsq, hipStream_t stream) {
+  DIONW_REQUIRE(count >= 0 && rows_per_tensor > 0 && cols > 0, "full_sumsq: bad sizes");
+  DIONW_REQUIRE(row_sumsq, "full_sumsq: null pointer");
+  for (int32_t start = 0; start < count; start += kMaxTensors) {
+    AccArgs a{};
+    a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
+    for (int i = 0; i < a.t.count; ++i) {
+      DIONW_REQUIRE(grads[start + i], "full_sumsq: null gradient %d", start + i);
+      a.t.grad[i] = grads[start + i];
+    }
+    const int64_t row0 = (int64_t)start * rows_per_tensor;
+    a.momentum = momentum ? const_cast<float*>(momentum) + row0 * cols : nullptr;
+    a.rowsq = row_sumsq + row0;
+    a.rows_per_tensor = rows_per_tensor;
+    a.cols = cols;
+    a.mu = mu;
+    a.nesterov = nesterov;
+    a.vec = table_aligned(a.t, cols) && (!a.momentum || aligned16(a.momentum));
+    const int64_t rows = (int64_t)a.t.count * rows_per_tensor;
+    hipLaunchKernelGGL(accumulate_kernel<kFullSumsq>,
+                       dim3((unsigned)ceil_div(rows, kRowsPerBlock)), dim3(256), 0, stream, a);
+    DIONW_TRY(check_launch("full_sumsq"));
+  }
+  return kOk;
+}
+
+int dionw_block_denom(const float* row_sumsq, int64_t blocks, int64_t rows, float safety,
+                      float eps, float* den, hipStream_t stream) {
+  DIONW_REQUIRE(row_sumsq && den && blocks >= 0 && rows > 0, "block_denom: bad arguments");
+  if (blocks == 0) return kOk;
+  hipLaunchKernelGGL(block_denom_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, row_sumsq,
+                     den, rows, safety, eps);
+  return check_launch("block_denom");
+}
+
+// See include/dionw_hip.h for the argument contract.
+int dionw_prepare_ns_input(const float* const* grads, int32_t count, float* momentum,
+                           const int32_t* idx, const float* den, int64_t blocks, int64_t rows,
+                           int64_t cols, int64_t k, int64_t p_pad, int64_t j_pad, float mu,
+                           int32_t nesterov, int32_t write_m, int32_t elem, void* out_rowmajor,
+                           void* out_transposed, hipStream_t stream) {
+  const bool full = idx == nullptr;
+  DIONW_REQUIRE(den && out_rowmajor, "prepare_ns_input: null pointer");
+  DIONW_REQUIRE(momentum || (idx == nullptr && !write_m),
+                "prepare_ns_input: only every-row mode without momentum writes may omit momentum");
+  DIONW_REQUIRE(blocks >= 0 && rows > 0 && cols > 0 && k > 0 && k <= rows,
+                "prepare_ns_input: bad sizes");
+  DIONW_REQUIRE(!full || k == rows, "prepare_ns_input: every-row mode needs k == rows");
+  DIONW_REQUIRE(elem == kF16 || elem == kBF16 || elem == kF32, "prepare_ns_input: bad elem %d",
+                elem);
+  if (blocks == 0) return kOk;
+  PrepArgs a{};
+  a.momentum = momentum;
+  a.idx = idx;
+  a.den = den;
+  a.out_r = out_rowmajor;
+  a.out_t = out_transposed;
+  a.rows = rows;
+  a.cols = cols;
+  a.k = k;
+  a.mu = mu;
+  a.full = full;
+  a.nesterov = nesterov;
+  a.write_m = write_m;
+  a.elem = elem;
+  if (full) {
+    DIONW_REQUIRE(count > 0 && count <= kMaxTensors && blocks % count == 0,
+                  "prepare_ns_input: every-row mode takes 1..%d gradients dividing the blocks",
+                  kMaxTensors);
+    a.t.count = count;
+    for (int i = 0; i < count; ++i) {
+      DIONW_REQUIRE(grads[i], "prepare_ns_input: null gradient %d", i);
+      a.t.grad[i] = grads[i];
+    }
+    a.blocks_per_tensor = blocks / count;
+  } else {
+    a.blocks_per_tensor = blocks;
+  }
+  a.vec = (cols % 4 == 0) && (!momentum || aligned16(momentum)) &&
+          (!full || table_aligned(a.t, cols));
+  if (elem == kF32) {
+    DIONW_REQUIRE(out_transposed == nullptr, "prepare_ns_input: fp32 output has no transpose");
+    a.p_pad = k;
+    a.j_pad = cols;
+    dim3 grid((unsigned)std::min<int64_t>(ceil_div(cols, 256), 64), (unsigned)k,
+              (unsigned)blocks);
+    hipLaunchKernelGGL(prepare_raw_kernel, grid, dim3(256), 0, stream, a);
+    return check_launch("prepare_ns_input");
+  }
+  DIONW_REQUIRE(p_pad >= k && j_pad >= cols && p_pad % 8 == 0 && j_pad % 8 == 0,
+                "prepare_ns_input: padded extents must cover the block and be multiples of 8");
+  a.p_pad = p_pad;
+  a.j_pad = j_pad;
+  dim3 grid((unsigned)ceil_div(j_pad, kTile), (unsigned)ceil_div(p_pad, kTile), (unsigned)blocks);
+  DIONW_REQUIRE(blocks <= 65535 && grid.y <= 65535, "prepare_ns_input: grid too large");
+  if (elem == kF16)
+    hipLaunchKernelGGL(prepare_kernel<kF16>, grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(prepare_kernel<kBF16>, grid, dim3(256), 0, stream, a);
+  return check_launch("prepare_ns_input");
+}
+
+}  // extern "C"

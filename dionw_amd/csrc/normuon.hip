@@ -1,0 +1,237 @@
+// Steps 4 and 5 of a Dion block update: NorMuon row normalization
+// (_row_normalization.py:41-60) and the weight update (_matrix_step.py:274-311).
+//
+//  row stats   per selected row: s = sum of O^2 (O the bf16 orthogonalized
+//              rows), v' = lerp(v, s / cols, 1 - beta2) written back into the
+//              bucket variance, d = sqrt(v') + 1e-8.
+//  block scale per block: ||O||_F / max(||O / d||_F, 1e-8) * step, with
+//              ||O / d||_F^2 taken as sum_rows s / d^2.
+//  apply       W = W * decay on every row (when weight decay is on), then on
+//              the selected rows W += (O / d) * scale, so that the update is
+//              never materialized in HBM.
+//
+// Contraction is off in this file: every product and sum rounds on its own,
+// as the reference's separate torch ops do.
+#pragma clang fp contract(off)
+
+#include "common.h"
+
+namespace dionw {
+namespace {
+
+struct StatArgs {
+  const __bf16* o;      // [B, k, cols]
+  float* variance;      // [B, rows] run variance (updated at the selected rows)
+  const int32_t* idx;   // [B, k] or nullptr (every row)
+  float* rowd;          // [B, k]
+  float* rows_s;        // [B, k]
+  float* rows_t;        // [B, k]
+  int64_t blocks, k, rows, cols;
+  float weight;         // 1 - beta2
+  int vec;
+};
+
+__global__ __launch_bounds__(256) void row_stats_kernel(StatArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.blocks * a.k) return;
+  const __bf16* o = a.o + r * a.cols;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (a.vec) {
+    const int64_t n8 = a.cols >> 3;
+    const bf16x8* o8 = reinterpret_cast<const bf16x8*>(o);
+    for (int64_t c = lane; c < n8; c += kWave) {
+      bf16x8 v = o8[c];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float x = (float)v[e], y = (float)v[e + 1];
+        acc[e >> 1] += x * x + y * y;
+      }
+    }
+  } else {
+    for (int64_t c = lane; c < a.cols; c += kWave) {
+      float x = (float)o[c];
+      acc.x += x * x;
+    }
+  }
+  const float s = wave_sum((acc.x + acc.y) + (acc.z + acc.w));
+  if (lane == 0) {
+    const int64_t b = r / a.k, p = r - b * a.k;
+    const int64_t vrow = b * a.rows + (a.idx ? (int64_t)a.idx[r] : p);
+    const float v = a.variance[vrow];
+    const float ms = s / (float)a.cols;
+    const float w = a.weight;
+    const float nv = w < 0.5f ? v + w * (ms - v) : ms - (ms - v) * (1.f - w);
+    a.variance[vrow] = nv;
+    const float d = sqrtf(nv) + 1e-8f;
+    a.rowd[r] = d;
+    a.rows_s[r] = s;
+    a.rows_t[r] = s / (d * d);
+  }
+}
+
+__global__ __launch_bounds__(64) void block_scale_kernel(const float* rows_s, const float* rows_t,
+                                                         float* scale, int64_t k, float step) {
+  const int64_t b = blockIdx.x;
+  float s = 0.f, t = 0.f;
+  for (int64_t i = threadIdx.x; i < k; i += kWave) {
+    s += rows_s[b * k + i];
+    t += rows_t[b * k + i];
+  }
+  s = wave_sum(s);
+  t = wave_sum(t);
+  if (threadIdx.x == 0) {
+    const float restore = sqrtf(s) / fmaxf(sqrtf(t), 1e-8f);
+    scale[b] = restore * step;
+  }
+}
+
+struct ApplyArgs {
+  RowTable t;             // parameters, rows_per_tensor rows of cols each
+  const __bf16* o;        // [B, k, cols]
+  const int32_t* slot;    // [B, rows] slot of each row or -1; nullptr: slot = row
+  const int32_t* idx;     // [B, k] (only_selected)
+  const float* rowd;      // [B, k] or nullptr (no row normalization)
+  const float* scale;     // [B] or nullptr (use step)
+  float step, decay;
+  int apply_decay, only_selected, vec;
+  int64_t rows_per_tensor, rows, cols, k;
+};
+
+__device__ __forceinline__ float update_one(float w, float o, float d, float s,
+                                            bool normalized, float decay, bool apply_decay) {
+  if (apply_decay) w = w * decay;
+  const float n = normalized ? o / d : o;
+  return w + n * s;
+}
+
+__global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int64_t gr, slot, b;
+  if (a.only_selected) {
+    const int64_t total = (int64_t)a.t.count * (a.rows_per_tensor / a.rows) * a.k;
+    if (r >= total) return;
+    b = r / a.k;
+    slot = r - b * a.k;
+    gr = b * a.rows + a.idx[r];
+  } else {
+    if (r >= (int64_t)a.t.count * a.rows_per_tensor) return;
+    gr = r;
+    b = gr / a.rows;
+    const int64_t in_block = gr - b * a.rows;
+    slot = a.slot ? (int64_t)a.slot[b * a.rows + in_block] : in_block;
+  }
+  const int tensor = (int)(gr / a.rows_per_tensor);
+  float* w = a.t.param[tensor] + (gr - (int64_t)tensor * a.rows_per_tensor) * a.cols;
+  const bool apply_decay = a.apply_decay != 0;
+  if (slot < 0) {
+    if (!apply_decay) return;
+    if (a.vec) {
+      f32x4* w4 = reinterpret_cast<f32x4*>(w);
+      for (int64_t c = lane; c < (a.cols >> 2); c += kWave) w4[c] = w4[c] * a.decay;
+    } else {
+      for (int64_t c = lane; c < a.cols; c += kWave) w[c] = w[c] * a.decay;
+    }
+    return;
+  }
+  const int64_t orow = b * a.k + slot;
+  const __bf16* o = a.o + orow * a.cols;
+  const bool normalized = a.rowd != nullptr;
+  const float d = normalized ? a.rowd[orow] : 1.f;
+  const float s = a.scale ? a.scale[b] : a.step;
+  if (a.vec) {
+    f32x4* w4 = reinterpret_cast<f32x4*>(w);
+    const bf16x4* o4 = reinterpret_cast<const bf16x4*>(o);
+    for (int64_t c = lane; c < (a.cols >> 2); c += kWave) {
+      f32x4 wv = w4[c];
+      bf16x4 ov = o4[c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        wv[e] = update_one(wv[e], (float)ov[e], d, s, normalized, a.decay, apply_decay);
+      w4[c] = wv;
+    }
+  } else {
+    for (int64_t c = lane; c < a.cols; c += kWave)
+      w[c] = update_one(w[c], (float)o[c], d, s, normalized, a.decay, apply_decay);
+  }
+}
+
+}  // namespace
+}  // namespace dionw
+
+using namespace dionw;
+
+extern "C" {
+
+int dionw_normuon_stats(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows,
+                        int64_t cols, const int32_t* idx, float* variance, float beta2,
+                        float step, float* rowd, float* scratch, float* scale,
+                        hipStream_t stream) {
+  DIONW_REQUIRE(orthogonal && variance && rowd && scratch && scale, "normuon_stats: null pointer");
+  DIONW_REQUIRE(k > 0 && k <= rows && cols > 0, "normuon_stats: bad sizes");
+  DIONW_REQUIRE(idx || k == rows, "normuon_stats: every-row mode needs k == rows");
+  if (blocks == 0) return kOk;
+  StatArgs a{};
+  a.o = reinterpret_cast<const __bf16*>(orthogonal);
+  a.variance = variance;
+  a.idx = idx;
+  a.rowd = rowd;
+  a.rows_s = scratch;
+  a.rows_t = scratch + blocks * k;
+  a.blocks = blocks;
+  a.k = k;
+  a.rows = rows;
+  a.cols = cols;
+  a.weight = 1.f - beta2;
+  a.vec = cols % 8 == 0 && aligned16(orthogonal);
+  hipLaunchKernelGGL(row_stats_kernel, dim3((unsigned)ceil_div(blocks * k, 4)), dim3(256), 0,
+                     stream, a);
+  DIONW_TRY(check_launch("normuon_stats"));
+  hipLaunchKernelGGL(block_scale_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, a.rows_s,
+                     a.rows_t, scale, k, step);
+  return check_launch("normuon_scale");
+}
+
+int dionw_apply_update(float* const* params, int32_t count, int64_t blocks_per_tensor,
+                       int64_t rows, int64_t cols, int64_t k, const void* orthogonal,
+                       const int32_t* idx, const int32_t* slot, const float* rowd,
+                       const float* scale, float step, float decay, int32_t apply_decay,
+                       hipStream_t stream) {
+  DIONW_REQUIRE(orthogonal && count >= 0 && blocks_per_tensor > 0 && rows > 0 && cols > 0 &&
+                    k > 0 && k <= rows,
+                "apply_update: bad arguments");
+  DIONW_REQUIRE(k == rows || (idx && slot), "apply_update: row selection needs idx and slot");
+  for (int32_t start = 0; start < count; start += kMaxTensors) {
+    ApplyArgs a{};
+    a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
+    bool aligned = cols % 4 == 0;
+    for (int i = 0; i < a.t.count; ++i) {
+      DIONW_REQUIRE(params[start + i], "apply_update: null parameter %d", start + i);
+      a.t.param[i] = params[start + i];
+      aligned = aligned && aligned16(params[start + i]);
+    }
+    const int64_t b0 = (int64_t)start * blocks_per_tensor;
+    a.o = reinterpret_cast<const __bf16*>(orthogonal) + b0 * k * cols;
+    a.idx = idx ? idx + b0 * k : nullptr;
+    a.slot = (slot && k < rows) ? slot + b0 * rows : nullptr;
+    a.rowd = rowd ? rowd + b0 * k : nullptr;
+    a.scale = scale ? scale + b0 : nullptr;
+    a.step = step;
+    a.decay = decay;
+    a.apply_decay = apply_decay;
+    a.rows_per_tensor = blocks_per_tensor * rows;
+    a.rows = rows;
+    a.cols = cols;
+    a.k = k;
+    a.vec = aligned && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;
+    a.only_selected = !apply_decay && k < rows;
+    const int64_t n = a.only_selected ? (int64_t)a.t.count * blocks_per_tensor * k
+                                      : (int64_t)a.t.count * a.rows_per_tensor;
+    hipLaunchKernelGGL(apply_kernel, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, stream, a);
+    DIONW_TRY(check_launch("apply_update"));
+  }
+  return kOk;
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+"""EMA shadow arithmetic: ``lerp`` toward the live weights.
+
+Reference: src/dionw/ema/_update.py:17-70. GPU float32 sources update through
+the multi-tensor HIP kernel (one launch per 48 tensors, torch's lerp
+arithmetic, so a constant parameter keeps a bit-exact shadow); other sources
+are upcast into transient float32 copies a bounded chunk at a time; CPU
+shadows (CPU EMA) use torch's CPU lerp.
+"""
+
+from __future__ import annotations
+
+from typing import Final
+
+import torch
+from torch import Tensor
+
+from dionw_amd import _lib
+
+__all__ = ["FP32", "ema_update_", "foreach_ema_copy_", "foreach_ema_update_"]
+
+FP32: Final[torch.dtype] = torch.float32
+_STAGING_CHUNK_NUMEL: Final[int] = 1 << 24
+
+
+def ema_update_(shadow: Tensor, source: Tensor, *, decay: float) -> None:
+    """``shadow = lerp(shadow, source, 1 - decay)`` in place (any device)."""
+    shadow.lerp_(source, 1.0 - decay)
+
+
+def _hip_lerp(shadows: list[Tensor], sources: list[Tensor], weight: float, copy: bool) -> None:
+    if not shadows:
+        return
+    _lib.call(
+        "dionw_ema_update",
+        _lib.ptr_array(shadows),
+        _lib.ptr_array(sources),
+        _lib.int64_array([s.numel() for s in shadows]),
+        len(shadows),
+        float(weight),
+        int(copy),
+        _lib.stream_handle(shadows[0].device),
+    )
+
+
+def _kernel_ready(shadow: Tensor, source: Tensor) -> bool:
+    # The kernel is element-wise over the storage: any dense layout works as
+    # long as both tensors share it (a channels-last weight and its shadow).
+    return (
+        shadow.is_cuda
+        and source.is_cuda
+        and source.dtype == FP32
+        and shadow.stride() == source.stride()
+        and shadow.is_non_overlapping_and_dense()
+        and source.is_non_overlapping_and_dense()
+    )
+
+
+@torch.no_grad()
+def foreach_ema_update_(shadows: list[Tensor], sources: list[Tensor], *, decay: float) -> None:
+    """``ema_update_`` over lists of shadows and sources.
+
+    Raises:
+        TypeError: If a shadow is not float32.
+        ValueError: If the lists differ in length.
+    """
+    if any(shadow.dtype != FP32 for shadow in shadows):
+        raise TypeError("EMA shadows must be float32")
+    if len(shadows) != len(sources):
+        raise ValueError("shadows and sources differ in length")
+    weight = 1.0 - decay
+    direct_s: list[Tensor] = []
+    direct_p: list[Tensor] = []
+    upcast: list[tuple[Tensor, Tensor]] = []
+    for shadow, source in zip(shadows, sources, strict=True):
+        if _kernel_ready(shadow, source):
+            direct_s.append(shadow)
+            direct_p.append(source)
+        elif shadow.is_cuda and source.is_cuda and shadow.is_non_overlapping_and_dense():
+            upcast.append((shadow, source))
+        else:
+            ema_update_(shadow, source.to(shadow.device, FP32), decay=decay)
+    _hip_lerp(direct_s, direct_p, weight, copy=False)
+    start = 0
+    while start < len(upcast):
+        stop, numel = start + 1, upcast[start][1].numel()
+        while stop < len(upcast) and numel + upcast[stop][1].numel() <= _STAGING_CHUNK_NUMEL:
+            numel += upcast[stop][1].numel()
+            stop += 1
+        chunk = upcast[start:stop]
+        staged = [torch.empty_like(shadow).copy_(source) for shadow, source in chunk]
+        _hip_lerp([s for s, _ in chunk], staged, weight, copy=False)
+        start = stop
+
+
+@torch.no_grad()
+def foreach_ema_copy_(shadows: list[Tensor], sources: list[Tensor]) -> None:
+    """Copy sources into shadows (the first update of a shadow)."""
+    direct_s: list[Tensor] = []
+    direct_p: list[Tensor] = []
+    for shadow, source in zip(shadows, sources, strict=True):
+        if _kernel_ready(shadow, source):
+            direct_s.append(shadow)
+            direct_p.append(source)
+        else:
+            shadow.copy_(source)
+    _hip_lerp(direct_s, direct_p, 1.0, copy=True)

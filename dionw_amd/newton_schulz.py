@@ -1,0 +1,164 @@
+"""The orthogonalization of Dion's matrix updates (``NewtonSchulz``).
+
+Reference: src/dionw/newton_schulz.py:30-68, the plugin boundary. Each kind
+maps a ``[N, rows, cols]`` batch (any float dtype) and the epsilon added to its
+Frobenius norm to the bfloat16 polar-factor approximations, five polynomial
+steps each, on the MFMA kernels of ``libdionw_hip.so``:
+
+- ``GRAM``: float16 Gram Newton-Schulz on ``X X^T`` with a restart at
+  iteration 2 (wide blocks; tall ones are transposed, square ones run the
+  standard Polar Express iteration), output bf16(fp16);
+- ``POLAR_EXPRESS`` / ``POLAR_EXPRESS_TRITON``: the bfloat16 Polar Express
+  quintic, input scaled by 1.02 times its norm;
+- ``KELLER`` / ``KELLER_TRITON``: Keller Jordan's bfloat16 quintic.
+
+The cuBLAS and Triton variants of the reference differ only in how their
+products round; here both run the same symmetric-product kernels.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+from dataclasses import dataclass
+from enum import Enum
+
+import torch
+from torch import Tensor
+
+from dionw_amd import _lib, _workspace
+
+__all__ = ["NewtonSchulz", "Orthogonalize", "HipOrthogonalize", "newton_schulz_fn"]
+
+# A batched orthogonalization: ([N, rows, cols] input, epsilon) -> bf16 output.
+Orthogonalize = Callable[[Tensor, float], Tensor]
+
+# Library kinds (include/dionw_hip.h, dionw_newton_schulz).
+_GRAM, _POLAR_EXPRESS, _KELLER = 0, 1, 2
+
+
+class NewtonSchulz(Enum):
+    """The orthogonalization of matrix updates."""
+
+    POLAR_EXPRESS = "polar_express"
+    POLAR_EXPRESS_TRITON = "polar_express_triton"
+    GRAM = "gram"
+    KELLER = "keller"
+    KELLER_TRITON = "keller_triton"
+
+
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+@dataclass(frozen=True)
+class HipOrthogonalize:
+    """One Newton-Schulz kind on the HIP kernels.
+
+    The optimizer feeds it straight from the momentum pass (the fused path);
+    called as a function it is the reference's ``Orthogonalize``.
+
+    Attributes:
+        kind: The ``NewtonSchulz`` kind.
+        lib_kind: The library's kind code.
+        dtype: Iteration dtype (float16 for Gram, bfloat16 for the quintics).
+        norm_safety: Factor on the Frobenius norm before normalizing.
+    """
+
+    kind: NewtonSchulz
+    lib_kind: int
+    dtype: torch.dtype
+    norm_safety: float
+
+    @property
+    def elem(self) -> int:
+        return _lib.elem_code(self.dtype)
+
+    def __call__(self, matrix: Tensor, epsilon: float) -> Tensor:
+        """Orthogonalize a ``[N, rows, cols]`` (or 2-D) batch; returns bfloat16.
+
+        Raises:
+            ValueError: For a tensor that is not 2-D or 3-D or not on a GPU.
+        """
+        if matrix.ndim not in (2, 3):
+            raise ValueError(f"expected a 2-D or 3-D batch, got {tuple(matrix.shape)}")
+        if not matrix.is_cuda:
+            raise ValueError("the HIP orthogonalization needs a GPU tensor")
+        batch3 = matrix if matrix.ndim == 3 else matrix.unsqueeze(0)
+        blocks, rows, cols = (int(d) for d in batch3.shape)
+        out = torch.empty(blocks, rows, cols, device=matrix.device, dtype=torch.bfloat16)
+        if blocks == 0:
+            return out if matrix.ndim == 3 else out[0]
+        source = batch3.to(torch.float32).contiguous()
+        device = source.device
+        stream = _lib.stream_handle(device)
+        rowsq = _workspace.buffer(device, "ortho_rowsq", (blocks * rows,), torch.float32)
+        den = _workspace.buffer(device, "ortho_den", (blocks,), torch.float32)
+        grads = _lib.ptr_array([source])
+        _lib.call("dionw_full_sumsq", grads, 1, blocks * rows, cols, None, 0.0, 0,
+                  rowsq.data_ptr(), stream)
+        _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, self.norm_safety,
+                  float(epsilon), den.data_ptr(), stream)
+        p_pad, j_pad = _round8(rows), _round8(cols)
+        xr = _workspace.buffer(device, "ortho_xr", (blocks, p_pad, j_pad), self.dtype)
+        xt = _workspace.buffer(device, "ortho_xt", (blocks, j_pad, p_pad), self.dtype)
+        _lib.call("dionw_prepare_ns_input", grads, 1, None, None, den.data_ptr(), blocks, rows,
+                  cols, rows, p_pad, j_pad, 0.0, 0, 0, self.elem, xr.data_ptr(), xt.data_ptr(),
+                  stream)
+        run_newton_schulz(self, blocks, rows, cols, xr, xt, out, stream)
+        return out if matrix.ndim == 3 else out[0]
+
+
+def run_newton_schulz(
+    ortho: HipOrthogonalize,
+    blocks: int,
+    rows: int,
+    cols: int,
+    xr: Tensor,
+    xt: Tensor,
+    out: Tensor,
+    stream: int,
+) -> None:
+    """Run the iteration on prepared inputs and write ``out`` ([blocks, rows, cols] bf16).
+
+    ``xr`` is the normalized input in the weight's orientation ([blocks,
+    round8(rows), round8(cols)]) and ``xt`` its transpose; a tall block
+    (rows > cols) iterates on the transpose. Both are overwritten.
+    """
+    tall = rows > cols
+    if tall:
+        x, x_t, r, c, r_real, c_real = xt, xr, _round8(cols), _round8(rows), cols, rows
+    else:
+        x, x_t, r, c, r_real, c_real = xr, xt, _round8(rows), _round8(cols), rows, cols
+    lib = _lib.library()
+    need = int(lib.dionw_newton_schulz_workspace(ortho.lib_kind, blocks, r, c))
+    ws = _workspace.buffer(out.device, "ns_workspace", (need,), torch.uint8)
+    _lib.call("dionw_newton_schulz", ortho.lib_kind, blocks, r, c, x.data_ptr(), x_t.data_ptr(),
+              r_real, c_real, out.data_ptr(), int(tall), cols, rows * cols, ws.data_ptr(), need,
+              stream)
+
+
+_KINDS: dict[NewtonSchulz, HipOrthogonalize] = {
+    NewtonSchulz.GRAM: HipOrthogonalize(NewtonSchulz.GRAM, _GRAM, torch.float16, 1.0),
+    NewtonSchulz.POLAR_EXPRESS: HipOrthogonalize(
+        NewtonSchulz.POLAR_EXPRESS, _POLAR_EXPRESS, torch.bfloat16, 1.02
+    ),
+    NewtonSchulz.POLAR_EXPRESS_TRITON: HipOrthogonalize(
+        NewtonSchulz.POLAR_EXPRESS_TRITON, _POLAR_EXPRESS, torch.bfloat16, 1.02
+    ),
+    NewtonSchulz.KELLER: HipOrthogonalize(NewtonSchulz.KELLER, _KELLER, torch.bfloat16, 1.0),
+    NewtonSchulz.KELLER_TRITON: HipOrthogonalize(
+        NewtonSchulz.KELLER_TRITON, _KELLER, torch.bfloat16, 1.0
+    ),
+}
+
+
+def newton_schulz_fn(kind: NewtonSchulz) -> Orthogonalize:
+    """The orthogonalization of ``kind``.
+
+    Raises:
+        RuntimeError: For an unhandled kind.
+    """
+    try:
+        return _KINDS[NewtonSchulz(kind)]
+    except KeyError:
+        raise RuntimeError(f"Unhandled NewtonSchulz: {kind}") from None

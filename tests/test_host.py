@@ -1,0 +1,139 @@
+"""Host-side logic and the C ABI's presence (no GPU needed).
+
+Restates the reference's routing table (tests/test_routing.py:38-190), config
+validation, EMA schedule known answers (tests/test_ema.py:141-205) and the
+structural checks of load_state_dict (tests/test_optimizer.py:776-798).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+from torch import nn
+
+import dionw_amd
+from dionw_amd import EMAConfig, Route, RouteKind, RouteReason, param_groups
+from dionw_amd import _lib
+from dionw_amd.optimizer import _check_structure, _with_pre_option_keys
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "dionw_hip.h"
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    declared = set(re.findall(r"^\w[\w\s\*]*?\b(dionw_\w+)\s*\(", HEADER.read_text(), re.M))
+    assert declared, "no declarations parsed"
+    assert declared == set(_lib.SIGNATURES), "ctypes table and header disagree"
+    lib = ctypes.CDLL(str(_lib.library_path()))
+    for name in declared:
+        assert hasattr(lib, name), f"{name} not exported"
+    assert _lib.library().dionw_abi_version() == 1
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path) -> None:
+    monkeypatch.setattr(_lib, "_PATH", tmp_path / "absent.so")
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(_lib.LibraryMissingError):
+        _lib.library()
+
+
+class _Tokens(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.cls_token = nn.Parameter(torch.zeros(1, 1, 64))
+        self.pos_embed = nn.Parameter(torch.zeros(1, 16, 64))
+
+
+class _Net(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.embed = nn.Embedding(100, 64)
+        self.tokens = _Tokens()
+        self.dw = nn.Conv2d(64, 64, 3, groups=64)
+        self.conv = nn.Conv2d(64, 32, 3)
+        self.fc = nn.Linear(64, 128)
+        self.narrow = nn.Linear(64, 4)
+        self.norm = nn.LayerNorm(64)
+
+
+def test_default_route_table() -> None:
+    groups, report = param_groups(_Net(), fraction=0.5, selection_min_dim=64)
+    reasons = {p.name: (p.kind, p.reason) for p in report.parameters}
+    assert reasons["embed.weight"] == (RouteKind.ADAMW, RouteReason.EMBEDDING)
+    assert reasons["tokens.cls_token"] == (RouteKind.ADAMW, RouteReason.LEARNED_TOKENS)
+    assert reasons["tokens.pos_embed"] == (RouteKind.ADAMW, RouteReason.EMBEDDING_NAME)
+    assert reasons["dw.weight"] == (RouteKind.ADAMW, RouteReason.GROUPED_CONVOLUTION)
+    assert reasons["conv.weight"] == (RouteKind.MATRIX, RouteReason.MATRIX)
+    assert reasons["fc.weight"] == (RouteKind.MATRIX, RouteReason.MATRIX)
+    assert reasons["fc.bias"] == (RouteKind.ADAMW, RouteReason.VECTOR)
+    assert reasons["narrow.weight"] == (RouteKind.ADAMW, RouteReason.NARROW)
+    assert reasons["norm.weight"] == (RouteKind.ADAMW, RouteReason.VECTOR)
+    kinds = [g["dion_route"] for g in groups]
+    assert kinds == sorted(kinds)  # adamw groups first
+    fractions = {p.name: p.fraction for p in report.parameters}
+    assert fractions["fc.weight"] == 0.5 and fractions["conv.weight"] == 1.0  # 32 < 64
+    decay = {id(p): g.get("weight_decay") for g in groups for p in g["params"]}
+    net_embed_decayed = [g for g in groups if any(p.shape == (100, 64) for p in g["params"])][0]
+    assert "weight_decay" not in net_embed_decayed  # embeddings are decayed by default
+    assert None in decay.values() and 0.0 in decay.values()
+    lines = report.lines()
+    assert lines[0] == "dionw parameter routing:"
+    assert any("adamw (embedding): embed.weight (100, 64)" in line for line in lines)
+
+
+def test_declared_routes_and_conflicts() -> None:
+    net = _Net()
+    groups, report = param_groups(net, routes={net.fc.weight: Route(RouteKind.MATRIX, num_heads=2)})
+    entry = {p.name: p for p in report.parameters}["fc.weight"]
+    assert entry.reason is RouteReason.DECLARED and entry.num_heads == 2
+    with pytest.raises(ValueError, match="does not divide"):
+        param_groups(net, routes={net.fc.weight: Route(RouteKind.MATRIX, num_heads=3)})
+    with pytest.raises(ValueError, match="MATRIX route"):
+        param_groups(net, routes={net.fc.bias: Route(RouteKind.MATRIX)})
+    with pytest.raises(ValueError):
+        Route(RouteKind.ADAMW, num_heads=2)
+    with pytest.raises(ValueError):
+        param_groups(net, fraction=0.0)
+
+
+def test_ema_config_validation_and_kats() -> None:
+    with pytest.raises(ValueError):
+        EMAConfig(decay=1.0)
+    with pytest.raises(ValueError):
+        EMAConfig(decay_final=0.99)
+    with pytest.raises(ValueError):
+        EMAConfig(power_gamma=1.0, decay_final=0.99, decay_ramp_steps=10)
+    ramp = EMAConfig(decay=0.9, decay_final=0.99, decay_ramp_steps=10)
+    assert ramp.decay_at_step(0) == pytest.approx(0.9)
+    assert ramp.decay_at_step(5) == pytest.approx(0.945)
+    assert ramp.decay_at_step(20) == pytest.approx(0.99)
+    power = EMAConfig(decay=0.999, power_gamma=6.94)
+    assert power.decay_at_step(0) == 0.0
+    assert power.decay_at_step(1) == 0.0
+    assert power.decay_at_step(100) == pytest.approx(0.99 ** 7.94)
+    assert power.decay_at_step(10**7) == pytest.approx(0.999)
+
+
+def test_dion_rejects_cpu_and_unrouted_params() -> None:
+    p = nn.Parameter(torch.zeros(8, 8))
+    with pytest.raises(ValueError, match="CUDA"):
+        dionw_amd.Dion([{"params": [p], "dion_route": "matrix"}], lr=1e-3)
+    with pytest.raises(ValueError, match="lr and weight_decay"):
+        dionw_amd.Dion([{"params": [p], "dion_route": "matrix"}], lr=-1.0)
+
+
+def test_structural_key_refusal() -> None:
+    saved = [{"dion_route": "matrix", "fraction": 0.25, "num_heads": None,
+              "newton_schulz": "gram"}]
+    current = [{"dion_route": "matrix", "fraction": 0.5, "num_heads": None,
+                "newton_schulz": "gram", "row_normalization": "normuon",
+                "momentum_form": "heavy_ball"}]
+    with pytest.raises(ValueError, match="'fraction'"):
+        _check_structure(_with_pre_option_keys(saved), current)
+    current[0]["fraction"] = 0.25
+    _check_structure(_with_pre_option_keys(saved), current)
+    with pytest.raises(ValueError, match="param groups"):
+        _check_structure(saved, current * 2)

@@ -1,0 +1,234 @@
+"""HIP kernels against the CPU oracle and torch, through the C ABI (GPU).
+
+Each test names its case in the assertion message. Bars: bit-exact for the
+momentum add, the l1 scores (fixed reduction order), the row index sets, the
+momentum decay, AdamW (vs torch._fused_adamw_) and the EMA (vs
+torch._foreach_lerp_); rounding-derived tolerances for the 16-bit products.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from dionw_amd import _kernels, _lib, _workspace
+from dionw_amd.newton_schulz import NewtonSchulz, newton_schulz_fn
+from oracle import dion_ref
+from tests.conftest import rel_fro
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.mark.parametrize(("rows", "cols"), [(37, 3000), (64, 4096), (5, 1408), (17, 1001), (3, 6)])
+def test_accumulate_scores_bit_exact(rows: int, cols: int) -> None:
+    g = _gen(0)
+    grad = torch.randn(rows, cols, generator=g)
+    mom = torch.randn(rows, cols, generator=g)
+    expected_m = mom + grad
+    expected_scores = dion_ref.row_l1_scores(expected_m.numpy())
+    grad_d, mom_d = grad.to(DEV), mom.to(DEV)
+    scores = torch.empty(rows, device=DEV)
+    _kernels.accumulate_row_l1(grad_d, mom_d, scores, cols)
+    torch.cuda.synchronize()
+    assert torch.equal(mom_d.cpu(), expected_m), f"M + G differs ({rows}x{cols})"
+    got = scores.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), expected_scores.view(np.uint32)), (
+        f"l1 scores not bit-exact ({rows}x{cols}), max diff {np.abs(got - expected_scores).max()}"
+    )
+    brute = np.abs(expected_m.double().numpy()).sum(-1)
+    np.testing.assert_allclose(got, brute, rtol=1e-5)
+
+
+def _select(scores: torch.Tensor, rowsq: torch.Tensor, k: int):
+    blocks, rows = scores.shape
+    idx = torch.empty(blocks, k, dtype=torch.int32, device=DEV)
+    slot = torch.empty(blocks, rows, dtype=torch.int32, device=DEV)
+    den = torch.empty(blocks, device=DEV)
+    _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k, 1.0,
+              1e-8, idx.data_ptr(), slot.data_ptr(), den.data_ptr(), _lib.stream_handle())
+    torch.cuda.synchronize()
+    return idx.cpu().numpy(), slot.cpu().numpy(), den.cpu()
+
+
+@pytest.mark.parametrize(("blocks", "rows", "k"), [(3, 1000, 250), (2, 14336, 3584), (4, 37, 37),
+                                                   (1, 5, 1), (2, 4096, 1024)])
+def test_select_rows_exact(blocks: int, rows: int, k: int) -> None:
+    g = _gen(1)
+    scores = torch.rand(blocks, rows, generator=g)
+    scores[0, : rows // 3] = scores[0, rows // 3]  # a block full of ties
+    rowsq = torch.rand(blocks, rows, generator=g)
+    idx, slot, den = _select(scores.to(DEV), rowsq.to(DEV), k)
+    for b in range(blocks):
+        expected = dion_ref.topk_rows(scores[b].numpy(), k)
+        assert np.array_equal(idx[b], expected), f"block {b}: index set differs ({rows}, {k})"
+        inverse = np.full(rows, -1)
+        inverse[expected] = np.arange(k)
+        assert np.array_equal(slot[b], inverse), f"block {b}: slot map differs"
+        ref_den = float(np.sqrt(rowsq[b].double().numpy()[expected].sum())) + 1e-8
+        assert abs(float(den[b]) - ref_den) <= 1e-5 * ref_den
+
+
+def test_select_rows_all_zero_scores() -> None:
+    """Zero gradients leave every score at 0: the first k rows are taken."""
+    scores = torch.zeros(2, 64, device=DEV)
+    idx, _, _ = _select(scores, torch.zeros_like(scores), 16)
+    assert np.array_equal(idx, np.tile(np.arange(16), (2, 1)))
+
+
+@pytest.mark.parametrize("nesterov", [False, True])
+def test_accumulate_copy_decay(nesterov: bool) -> None:
+    g = _gen(2)
+    grad, mom = torch.randn(5001, generator=g), torch.randn(5001, generator=g)
+    s = mom + grad
+    decayed = s * 0.95
+    expected_out = grad + decayed if nesterov else s
+    grad_d, mom_d = grad.to(DEV), mom.to(DEV)
+    out = torch.empty(5001, device=DEV)
+    _kernels.accumulate_copy_decay(grad_d, mom_d, out, 0.95, nesterov=nesterov)
+    torch.cuda.synchronize()
+    assert torch.equal(mom_d.cpu(), decayed), "decayed momentum not bit-exact"
+    assert torch.equal(out.cpu(), expected_out), "Newton-Schulz input not bit-exact"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(("batch", "m", "n", "k"), [(1, 64, 64, 64), (3, 100, 72, 136),
+                                                    (2, 256, 512, 1024), (5, 352, 352, 2048)])
+def test_gemm_nt_matches_fp32(dtype: torch.dtype, batch: int, m: int, n: int, k: int) -> None:
+    g = _gen(3)
+    a = torch.randn(batch, m, k, generator=g).to(dtype)
+    b = torch.randn(batch, n, k, generator=g).to(dtype)
+    d = torch.randn(batch, m, n, generator=g).to(dtype)
+    expected = (0.7 * (a.float() @ b.float().mT) - 1.3 * d.float()).to(dtype)
+    out = torch.empty(batch, m, n, dtype=dtype, device=DEV)
+    out_t = torch.empty(batch, n, m, dtype=dtype, device=DEV)
+    _kernels.gemm_nt(a.to(DEV), b.to(DEV), d=d.to(DEV), alpha=0.7, beta=-1.3, out=out, out_t=out_t)
+    torch.cuda.synchronize()
+    tol = 2e-3 if dtype == torch.float16 else 1e-2
+    err = rel_fro(out.cpu(), expected)
+    assert err < tol, f"gemm {batch}x{m}x{n}x{k} {dtype}: rel err {err}"
+    assert torch.equal(out_t.cpu(), out.cpu().mT), "transposed store differs"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(3, 64, 256), (3, 128, 128), (96, 160), (2, 520, 1032)])
+def test_symmetric_products(dtype: torch.dtype, shape: tuple[int, ...]) -> None:
+    g = _gen(4)
+    x = (torch.randn(*shape, generator=g) / shape[-1] ** 0.5).to(dtype)
+    gram = _kernels.ns_line_1(x.to(DEV))
+    torch.cuda.synchronize()
+    ref = dion_ref.ns_line_1(x)
+    tol = 2e-3 if dtype == torch.float16 else 1e-2
+    assert rel_fro(gram.cpu(), ref) < tol, f"ns_line_1 {shape} {dtype}"
+    assert torch.equal(gram.cpu(), gram.cpu().mT), "ns_line_1 output not exactly symmetric"
+    poly = _kernels.ns_line_2(gram, alpha=0.5, beta=-1.5)
+    torch.cuda.synchronize()
+    ref2 = dion_ref.ns_line_2(gram.cpu(), 0.5, -1.5)
+    assert rel_fro(poly.cpu(), ref2) < tol, f"ns_line_2 {shape} {dtype}"
+    assert torch.equal(poly.cpu(), poly.cpu().mT)
+
+
+NS_SHAPES = [(3, 64, 256), (3, 256, 64), (3, 128, 128), (2, 96, 160), (4, 256, 1024), (1, 352, 2048)]
+
+
+@pytest.mark.parametrize("shape", NS_SHAPES)
+@pytest.mark.parametrize("kind", list(NewtonSchulz))
+def test_newton_schulz_matches_oracle(kind: NewtonSchulz, shape: tuple[int, ...]) -> None:
+    g = _gen(5)
+    x = torch.randn(*shape, generator=g)
+    out = newton_schulz_fn(kind)(x.to(DEV), 1e-7)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and out.shape == x.shape
+    ref = dion_ref.ORTHOGONALIZE[kind.value](x, 1e-7)
+    err = rel_fro(out.cpu().float(), ref.float())
+    # Both round to float16/bfloat16 at the same points; they differ by the
+    # accumulation order of the products and the mirrored symmetric tiles.
+    bar = 1e-2 if kind is NewtonSchulz.GRAM else 3e-2
+    assert err < bar, f"{kind.value} {shape}: rel err vs oracle {err}"
+    # Keller's quintic pushes singular values into about [0.7, 1.2], not onto 1.
+    polar_bar = 0.3 if kind in (NewtonSchulz.KELLER, NewtonSchulz.KELLER_TRITON) else 0.2
+    exact_err = rel_fro(out.cpu().float(), dion_ref.exact_polar(x))
+    assert exact_err < polar_bar, f"{kind.value} {shape}: {exact_err} from the exact polar factor"
+
+
+@pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 1024, 4096)])
+def test_gram_rounding_error_vs_float64_polynomial(shape: tuple[int, ...]) -> None:
+    """Rounding error of the fp16 Gram iteration against the same polynomial in
+    float64 (bench/precision.py method; the reference measures 0.003 on
+    Gaussian 256 x 1024 input)."""
+    g = _gen(6)
+    x = torch.randn(*shape, generator=g)
+    out = newton_schulz_fn(NewtonSchulz.GRAM)(x.to(DEV), 1e-7)
+    torch.cuda.synchronize()
+    target = dion_ref.polynomial_float64(x, dion_ref.GRAM_COEFFICIENTS, 1.0)
+    err = rel_fro(out.cpu().float(), target)
+    oracle_err = rel_fro(dion_ref.gram_polar_express(x, 1e-7).float(), target)
+    assert err < 1.3 * oracle_err + 3e-3, f"{shape}: gpu {err} vs oracle {oracle_err}"
+    assert err < 0.01
+
+
+def test_adamw_bit_exact_vs_torch_fused() -> None:
+    from dionw_amd._adamw import adamw_step, init_adamw_state
+
+    g = _gen(7)
+    shapes = [(1000,), (37, 61), (4096, 3), (1,), (70000,)]
+    params = [torch.randn(*s, generator=g).to(DEV) for s in shapes]
+    ref_params = [p.clone() for p in params]
+    state: dict = {}
+    for p in params:
+        state[p] = {}
+        init_adamw_state(p, state[p])
+    ref_m = [torch.zeros_like(p) for p in params]
+    ref_v = [torch.zeros_like(p) for p in params]
+    ref_steps = [torch.zeros((), device=DEV) for _ in params]
+    group = {"params": params, "lr": 3e-4, "betas": (0.9, 0.95), "weight_decay": 0.05, "eps": 1e-8}
+    for it in range(4):
+        grads = [torch.randn(*s, generator=g).to(DEV) * 1e-3 for s in shapes]
+        for p, gr in zip(params, grads):
+            p.grad = gr.clone()
+        adamw_step(group, state)
+        torch._foreach_add_(ref_steps, 1)
+        torch._fused_adamw_(ref_params, grads, ref_m, ref_v, [], ref_steps, amsgrad=False,
+                            lr=3e-4, beta1=0.9, beta2=0.95, weight_decay=0.05, eps=1e-8,
+                            maximize=False, grad_scale=None, found_inf=None)
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            assert torch.equal(p, ref_params[i]), f"step {it} tensor {i}: param not bit-exact"
+            assert torch.equal(state[p]["exp_avg"], ref_m[i]), f"step {it} tensor {i}: exp_avg"
+            assert torch.equal(state[p]["exp_avg_sq"], ref_v[i]), f"step {it} tensor {i}: exp_avg_sq"
+            assert torch.equal(state[p]["adamw_step"], ref_steps[i])
+
+
+@pytest.mark.parametrize("decay", [0.9999, 0.3, 0.5])
+def test_ema_bit_exact_vs_torch_lerp(decay: float) -> None:
+    from dionw_amd.ema._update import foreach_ema_copy_, foreach_ema_update_
+
+    g = _gen(8)
+    shapes = [(1000,), (37, 61), (70001,)]
+    shadows = [torch.randn(*s, generator=g).to(DEV) for s in shapes]
+    sources = [torch.randn(*s, generator=g).to(DEV) for s in shapes]
+    ref = [s.clone() for s in shadows]
+    foreach_ema_update_(shadows, sources, decay=decay)
+    torch._foreach_lerp_(ref, sources, 1.0 - decay)
+    torch.cuda.synchronize()
+    for i in range(len(shapes)):
+        assert torch.equal(shadows[i], ref[i]), f"lerp tensor {i} decay {decay}"
+    constant = [s.clone() for s in sources]
+    foreach_ema_update_(constant, sources, decay=decay)
+    for c, s in zip(constant, sources):
+        assert torch.equal(c, s), "a constant source must keep a bit-exact shadow"
+    copies = [torch.empty_like(s) for s in sources]
+    foreach_ema_copy_(copies, sources)
+    for c, s in zip(copies, sources):
+        assert torch.equal(c, s)
+
+
+def test_workspace_is_reused() -> None:
+    a = _workspace.buffer(torch.device(DEV), "t", (10,), torch.float32)
+    b = _workspace.buffer(torch.device(DEV), "t", (5,), torch.float32)
+    assert a.data_ptr() == b.data_ptr()

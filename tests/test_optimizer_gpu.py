@@ -1,0 +1,292 @@
+"""``Dion.step`` on the HIP path against the CPU oracle and the reference's invariants (GPU).
+
+Restates the reference's optimizer tests (tests/test_optimizer.py) without
+microsoft/dion: the Newton-Schulz plugin is replaced by the exact polar factor
+(as test_optimizer.py:90-132 does) to pin every other stage to float32
+rounding, and the HIP Newton-Schulz is checked against the oracle's.
+"""
+
+from __future__ import annotations
+
+import io
+import math
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import dionw_amd
+import dionw_amd._buckets
+from dionw_amd import (
+    FRACTION_KEY,
+    NUM_HEADS_KEY,
+    ROUTE_KEY,
+    Dion,
+    EMAConfig,
+    MatrixUpdate,
+    MomentumForm,
+    NewtonSchulz,
+    RouteKind,
+    RowNormalization,
+)
+from oracle import dion_ref
+from tests.conftest import rel_fro
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+LR = 1e-3
+
+
+def _exact_polar_bf16(x: torch.Tensor, epsilon: float) -> torch.Tensor:
+    del epsilon
+    return dion_ref.exact_polar(x.cpu()).to(device=x.device, dtype=torch.bfloat16)
+
+
+def _dion(params, fraction, *, kind=NewtonSchulz.GRAM, weight_decay=0.0, normuon=True,
+          nesterov=False, heads=None, ema=None) -> Dion:
+    return Dion(
+        [{"params": list(params), ROUTE_KEY: RouteKind.MATRIX.value, FRACTION_KEY: fraction,
+          NUM_HEADS_KEY: heads}],
+        lr=LR, momentum=0.95, muon_beta2=0.95, betas=(0.9, 0.99), weight_decay=weight_decay,
+        eps=1e-8,
+        matrix_update=MatrixUpdate(
+            kind,
+            RowNormalization.NORMUON if normuon else RowNormalization.NONE,
+            MomentumForm.NESTEROV if nesterov else MomentumForm.HEAVY_BALL,
+        ),
+        ema=ema,
+    )
+
+
+CASES = [((256, 512), 0.25), ((64, 128), 1.0), ((64, 128), 0.5), ((256, 64), 0.5),
+         ((128, 128), 0.25), ((160, 96), 1.0)]
+
+
+@pytest.mark.parametrize("weight_decay", [0.0, 0.1])
+@pytest.mark.parametrize(("shape", "fraction"), CASES)
+def test_exact_polar_step_matches_oracle(shape, fraction, weight_decay, monkeypatch) -> None:
+    """With Newton-Schulz replaced by the exact polar factor, the GPU step and
+    the oracle agree to float32 rounding over 4 steps (two same-shape params)."""
+    monkeypatch.setattr(dionw_amd._buckets, "newton_schulz_fn", lambda _kind: _exact_polar_bf16)
+    g = torch.Generator().manual_seed(0)
+    starts = [torch.randn(*shape, generator=g) * 0.02 for _ in range(2)]
+    params = [nn.Parameter(s.clone().to(DEV)) for s in starts]
+    opt = _dion(params, fraction, weight_decay=weight_decay)
+    rows, cols = shape
+    k = min(rows, math.ceil(fraction * rows))
+    w = torch.stack(starts)
+    mom = torch.zeros_like(w)
+    var = torch.zeros(2, rows, 1)
+    for step in range(4):
+        grads = torch.randn(2, *shape, generator=g)
+        for p, gr in zip(params, grads):
+            p.grad = gr.to(DEV)
+        opt.step()
+        dion_ref.step_blocks(w, grads, mom, var, k=k, lr=LR, mu=0.95, beta2=0.95,
+                             weight_decay=weight_decay, orthogonalize=_exact_polar_cpu)
+        got_m = torch.stack([opt.state[p]["momentum"].cpu() for p in params])
+        assert torch.equal(got_m, mom), f"step {step}: momentum differs (selection?)"
+        got_w = torch.stack([p.detach().cpu() for p in params])
+        torch.testing.assert_close(got_w, w, rtol=0, atol=2e-7, msg=f"step {step}: weights")
+
+
+def _exact_polar_cpu(x: torch.Tensor, epsilon: float) -> torch.Tensor:
+    del epsilon
+    return dion_ref.exact_polar(x).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("kind", [NewtonSchulz.GRAM, NewtonSchulz.POLAR_EXPRESS, NewtonSchulz.KELLER_TRITON])
+@pytest.mark.parametrize(("shape", "fraction", "heads"), [((1024, 1024), 1.0, None), ((512, 1024), 0.25, None),
+                                                          ((768, 256), 1.0, 3), ((1408, 512), 0.25, None)])
+def test_hip_step_matches_oracle(kind, shape, fraction, heads) -> None:
+    """The full HIP step (Newton-Schulz included) against the oracle: selection
+    and momentum bit-exact, the update within the Newton-Schulz rounding."""
+    g = torch.Generator().manual_seed(1)
+    start = torch.randn(*shape, generator=g) * 0.02
+    param = nn.Parameter(start.clone().to(DEV))
+    opt = _dion([param], fraction, kind=kind, weight_decay=0.05, heads=heads)
+    blocks = heads or 1
+    rows, cols = shape[0] // blocks, shape[1]
+    k = min(rows, math.ceil(fraction * rows))
+    w = start.view(blocks, rows, cols).clone()
+    mom = torch.zeros_like(w)
+    var = torch.zeros(blocks, rows, 1)
+    for step in range(3):
+        grad = torch.randn(*shape, generator=g) * 1e-3
+        param.grad = grad.to(DEV)
+        before = param.detach().cpu().view(blocks, rows, cols).clone()
+        opt.step()
+        w_ref_before = w.clone()
+        dion_ref.step_blocks(w, grad.view(blocks, rows, cols), mom, var, k=k, lr=LR, mu=0.95,
+                             beta2=0.95, weight_decay=0.05, kind=kind.value)
+        got_m = opt.state[param]["momentum"].cpu().view(blocks, rows, cols)
+        assert torch.equal(got_m, mom), f"step {step}: momentum (selection) differs"
+        decay = 1.0 - LR * 0.05
+        upd_gpu = param.detach().cpu().view(blocks, rows, cols) - before * decay
+        upd_ref = w - w_ref_before * decay
+        err = rel_fro(upd_gpu, upd_ref)
+        assert err < 1e-2, f"step {step} {kind.value} {shape}: update rel err {err}"
+        assert rel_fro(param.detach().cpu().view(blocks, rows, cols), w) < 2e-3
+        got_v = opt.state[param]["variance"].cpu().view(blocks, rows, 1)
+        assert rel_fro(got_v, var) < 2e-2, f"step {step}: variance"
+        w = param.detach().cpu().view(blocks, rows, cols).clone()  # follow the GPU trajectory
+
+
+def test_lr_zero_freezes_weights() -> None:
+    g = torch.Generator().manual_seed(2)
+    param = nn.Parameter((torch.randn(128, 256, generator=g) * 0.02).to(DEV))
+    start = param.detach().clone()
+    opt = Dion([{"params": [param], ROUTE_KEY: "matrix", FRACTION_KEY: 0.5}], lr=0.0,
+               weight_decay=0.1)
+    for _ in range(2):
+        param.grad = torch.randn(128, 256, generator=g).to(DEV)
+        opt.step()
+    assert torch.equal(param.detach(), start)
+
+
+def test_weight_decay_exact_on_zero_gradients() -> None:
+    param = nn.Parameter(torch.randn(64, 128).to(DEV) * 0.02)
+    start = param.detach().clone()
+    opt = Dion([{"params": [param], ROUTE_KEY: "matrix", FRACTION_KEY: 0.5}], lr=1e-2,
+               weight_decay=0.1)
+    param.grad = torch.zeros_like(param)
+    opt.step()
+    assert torch.equal(param.detach(), start * (1.0 - 1e-2 * 0.1))
+
+
+def test_same_shape_momenta_share_storage() -> None:
+    params = [nn.Parameter(torch.randn(32, 32, device=DEV)) for _ in range(2)]
+    opt = _dion(params, 1.0)
+    for p in params:
+        p.grad = torch.randn_like(p)
+    opt.step()
+    storages = {opt.state[p]["momentum"].untyped_storage().data_ptr() for p in params}
+    assert len(storages) == 1
+    assert opt.state[params[0]]["momentum"].untyped_storage().nbytes() == 2 * 32 * 32 * 4
+
+
+def test_resume_is_bit_exact() -> None:
+    def model():
+        torch.manual_seed(3)
+        return nn.Sequential(nn.Linear(256, 512), nn.GELU(), nn.Linear(512, 128)).to(DEV)
+
+    def run(steps, opt, m, g):
+        for _ in range(steps):
+            for p in m.parameters():
+                p.grad = torch.randn(p.shape, generator=g).to(DEV) * 1e-3
+            opt.step()
+
+    m1 = model()
+    groups, _ = dionw_amd.param_groups(m1, fraction=0.5, selection_min_dim=128)
+    o1 = Dion(groups, lr=1e-3, weight_decay=0.05, ema=EMAConfig(decay=0.9))
+    run(4, o1, m1, torch.Generator().manual_seed(9))
+
+    m2 = model()
+    groups, _ = dionw_amd.param_groups(m2, fraction=0.5, selection_min_dim=128)
+    o2 = Dion(groups, lr=1e-3, weight_decay=0.05, ema=EMAConfig(decay=0.9))
+    gen = torch.Generator().manual_seed(9)
+    run(2, o2, m2, gen)
+    buf = io.BytesIO()
+    torch.save({"model": m2.state_dict(), "opt": o2.state_dict()}, buf)
+    buf.seek(0)
+    saved = torch.load(buf, weights_only=True)
+    m3 = model()
+    m3.load_state_dict(saved["model"])
+    groups, _ = dionw_amd.param_groups(m3, fraction=0.5, selection_min_dim=128)
+    o3 = Dion(groups, lr=1e-3, weight_decay=0.05, ema=EMAConfig(decay=0.9))
+    o3.load_state_dict(saved["opt"])
+    run(2, o3, m3, gen)
+    for a, b in zip(m1.parameters(), m3.parameters()):
+        assert torch.equal(a, b)
+    for a, b in zip(m1.parameters(), m3.parameters()):
+        assert torch.equal(o1.state[a]["ema_shadow"], o3.state[b]["ema_shadow"])
+
+
+def test_adamw_route_matches_torch_fused_adamw() -> None:
+    torch.manual_seed(4)
+    vec = nn.Parameter(torch.randn(300, device=DEV))
+    ref = nn.Parameter(vec.detach().clone())
+    opt = Dion([{"params": [vec], ROUTE_KEY: "adamw"}], lr=1e-3, betas=(0.9, 0.99),
+               weight_decay=0.1, eps=1e-8)
+    torch_opt = torch.optim.AdamW([ref], lr=1e-3, betas=(0.9, 0.99), weight_decay=0.1, eps=1e-8,
+                                  fused=True)
+    for _ in range(5):
+        grad = torch.randn(300, device=DEV)
+        vec.grad, ref.grad = grad.clone(), grad.clone()
+        opt.step()
+        torch_opt.step()
+        assert torch.equal(vec, ref)
+
+
+def test_runs_split_by_missing_gradients_match_lone_params() -> None:
+    g = torch.Generator().manual_seed(5)
+    starts = [torch.randn(64, 96, generator=g) * 0.02 for _ in range(3)]
+    grads = [torch.randn(64, 96, generator=g) for _ in range(3)]
+    together = [nn.Parameter(s.clone().to(DEV)) for s in starts]
+    opt = _dion(together, 0.5)
+    together[0].grad, together[2].grad = grads[0].to(DEV), grads[2].to(DEV)
+    opt.step()
+    for i in (0, 2):
+        lone = nn.Parameter(starts[i].clone().to(DEV))
+        lone_opt = _dion([lone], 0.5)
+        lone.grad = grads[i].to(DEV)
+        lone_opt.step()
+        assert torch.equal(lone.detach(), together[i].detach()), f"param {i}"
+    assert torch.equal(together[1].detach().cpu(), starts[1])
+
+
+def test_head_split_equals_separate_heads() -> None:
+    g = torch.Generator().manual_seed(6)
+    start = torch.randn(3 * 64, 128, generator=g) * 0.02
+    grad = torch.randn(3 * 64, 128, generator=g)
+    fused = nn.Parameter(start.clone().to(DEV))
+    opt = _dion([fused], 0.5, heads=3)
+    fused.grad = grad.to(DEV)
+    opt.step()
+    heads = [nn.Parameter(start[i * 64:(i + 1) * 64].clone().to(DEV)) for i in range(3)]
+    opt2 = _dion(heads, 0.5)
+    for i, h in enumerate(heads):
+        h.grad = grad[i * 64:(i + 1) * 64].to(DEV)
+    opt2.step()
+    assert torch.equal(fused.detach(), torch.cat([h.detach() for h in heads]))
+
+
+def test_gpu_ema_schedule() -> None:
+    torch.manual_seed(7)
+    p = nn.Parameter(torch.randn(100, device=DEV))
+    opt = Dion([{"params": [p], ROUTE_KEY: "adamw"}], lr=1e-2,
+               ema=EMAConfig(decay=0.9, update_every_n_steps=2))
+    expected = None
+    for step in range(1, 7):
+        p.grad = torch.randn_like(p)
+        opt.step()
+        if step % 2 == 0:
+            if expected is None:
+                expected = p.detach().clone()
+            else:
+                expected = torch.lerp(expected, p.detach(), 1 - 0.9**2)
+    torch.testing.assert_close(opt.state[p]["ema_shadow"], expected, rtol=1e-6, atol=0)
+
+
+def test_muon_update_matches_oracle() -> None:
+    """MUON_UPDATE: Nesterov momentum, Keller quintic, no row normalization."""
+    g = torch.Generator().manual_seed(8)
+    start = torch.randn(256, 384, generator=g) * 0.02
+    param = nn.Parameter(start.clone().to(DEV))
+    opt = _dion([param], 1.0, kind=NewtonSchulz.KELLER_TRITON, normuon=False, nesterov=True,
+                weight_decay=0.05)
+    w = start[None].clone()
+    mom = torch.zeros_like(w)
+    var = torch.zeros(1, 256, 1)
+    for step in range(3):
+        grad = torch.randn(256, 384, generator=g) * 1e-3
+        param.grad = grad.to(DEV)
+        before = param.detach().cpu().clone()
+        opt.step()
+        w = before[None].clone()
+        dion_ref.step_blocks(w, grad[None], mom, var, k=256, lr=LR, mu=0.95, beta2=0.95,
+                             weight_decay=0.05, kind="keller_triton", normuon=False, nesterov=True)
+        assert torch.equal(opt.state[param]["momentum"].cpu()[None], mom)
+        assert rel_fro(param.detach().cpu() - before * (1 - LR * 0.05),
+                       w[0] - before * (1 - LR * 0.05)) < 3e-2, f"step {step}"
