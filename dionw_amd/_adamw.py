@@ -15,6 +15,7 @@ from torch import Tensor
 
 from dionw_amd import _lib
 from dionw_amd._keys import ADAMW_STEP_STATE, EXP_AVG_SQ_STATE, EXP_AVG_STATE, ParamState
+from dionw_amd._layout import same_dense_layout
 
 __all__ = ["adamw_step", "init_adamw_state"]
 
@@ -24,10 +25,6 @@ def init_adamw_state(param: Tensor, state: dict[str, Any]) -> None:
     state[EXP_AVG_STATE] = torch.zeros_like(param)
     state[EXP_AVG_SQ_STATE] = torch.zeros_like(param)
     state[ADAMW_STEP_STATE] = torch.zeros((), dtype=torch.float32, device=param.device)
-
-
-def _dense_like(tensor: Tensor, reference: Tensor) -> bool:
-    return tensor.stride() == reference.stride() and tensor.is_non_overlapping_and_dense()
 
 
 def adamw_step(group: dict[str, Any], state: ParamState) -> None:
@@ -57,7 +54,7 @@ def adamw_step(group: dict[str, Any], state: ParamState) -> None:
         data = param.data
         m, v = entry[EXP_AVG_STATE], entry[EXP_AVG_SQ_STATE]
         grad = grad.to(torch.float32)
-        if not (data.is_non_overlapping_and_dense() and all(_dense_like(t, data) for t in (grad, m, v))):
+        if not all(same_dense_layout(t, data) for t in (grad, m, v)):
             # Mixed layouts: step row-major copies and write them back.
             flat = [t.contiguous() for t in (data, m, v)]
             copies.extend(zip((data, m, v), flat, strict=True))

@@ -15,6 +15,7 @@ import torch
 from torch import Tensor
 
 from dionw_amd import _lib
+from dionw_amd._layout import dense, same_dense_layout
 
 __all__ = ["FP32", "ema_update_", "foreach_ema_copy_", "foreach_ema_update_"]
 
@@ -45,14 +46,7 @@ def _hip_lerp(shadows: list[Tensor], sources: list[Tensor], weight: float, copy:
 def _kernel_ready(shadow: Tensor, source: Tensor) -> bool:
     # The kernel is element-wise over the storage: any dense layout works as
     # long as both tensors share it (a channels-last weight and its shadow).
-    return (
-        shadow.is_cuda
-        and source.is_cuda
-        and source.dtype == FP32
-        and shadow.stride() == source.stride()
-        and shadow.is_non_overlapping_and_dense()
-        and source.is_non_overlapping_and_dense()
-    )
+    return shadow.is_cuda and source.is_cuda and source.dtype == FP32 and same_dense_layout(shadow, source)
 
 
 @torch.no_grad()
@@ -75,7 +69,7 @@ def foreach_ema_update_(shadows: list[Tensor], sources: list[Tensor], *, decay: 
         if _kernel_ready(shadow, source):
             direct_s.append(shadow)
             direct_p.append(source)
-        elif shadow.is_cuda and source.is_cuda and shadow.is_non_overlapping_and_dense():
+        elif shadow.is_cuda and source.is_cuda and dense(shadow) and shadow.shape == source.shape:
             upcast.append((shadow, source))
         else:
             ema_update_(shadow, source.to(shadow.device, FP32), decay=decay)
