@@ -47,6 +47,13 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
+struct Problem {
+  int elem;  // kF16 / kBF16
+  int out_mode;
+  int64_t batch;
+  GemmArgs g;
+};
+
 template <typename T>
 struct Mfma;
 template <>
@@ -260,14 +267,466 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmArgs g) {
   }
 }
 
+// ---- pipelined large-tile kernel ------------------------------------------------
+//
+// 256x256 output tile per workgroup of 4 waves (2x2, 128x128 per wave: 16
+// accumulators of 32x32 in AGPRs, one wave per SIMD). k advances 32 at a time
+// through a 4-stage LDS ring filled by direct-to-LDS loads
+// (global_load_lds_dwordx4): a stage is requested three stages before it is
+// consumed, so HBM latency hides behind ~3000 cycles of MFMA work. Waits are
+// explicit: before a stage is read every wave waits for its own loads of it
+// (vmcnt) and for its reads of the stage about to be refilled (lgkmcnt), then
+// the workgroup meets at one barrier. Rows beyond m / n load a clamped valid
+// row (only outputs that are never stored see them), so every wave issues the
+// same number of loads per stage and the vmcnt arithmetic is exact; k must be
+// a multiple of 32.
+
+constexpr int PBK = 32;  // k depth of one LDS stage
+
+// Tile configuration: BM x BN output tile, WM x WN waves, STAGES-deep LDS ring.
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_>
+struct PipeCfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_;
+  static constexpr int threads = WM * WN * 64;
+  static constexpr int stage_elems = (BM + BN) * PBK;         // A then B
+  static constexpr int loads_a = BM * PBK / 8 / threads;      // 16-byte loads per thread
+  static constexpr int loads_b = BN * PBK / 8 / threads;
+  static constexpr size_t lds_bytes = (size_t)STAGES * stage_elems * 2;
+  static_assert(loads_a >= 1 && loads_b >= 1, "tile too small for the thread count");
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Chunk q (16 bytes, 0..3) of row r sits at q ^ ((r >> 2) & 3): the 16 lanes
+// of a read phase (rows r..r+15, same chunk) cover all 64 banks once.
+__device__ __forceinline__ int plds_off(int row, int chunk) {
+  return row * PBK + ((chunk ^ ((row >> 2) & 3)) << 3);
+}
+
+// ---- LDS-staged epilogue of the large-tile kernels ------------------------------
+//
+// The output tile (BM x BN, 16-bit) is assembled in LDS, so that every global
+// access is a 16-byte vector per lane: the addend D is loaded row by row,
+// each lane forms alpha * acc + beta * D for its fragment elements and rounds
+// once, then rows are stored straight (C, and C + shift I) and columns are
+// gathered for the transposed / mirrored store (CT). The tile row stride
+// ELD = BN + 8 keeps rows 16-byte aligned.
+
+template <int BN>
+constexpr int epi_ld() { return BN + 8; }
+
+template <int BM, int BN>
+constexpr size_t epi_lds_bytes() { return (size_t)BM * epi_ld<BN>() * 2; }
+
+template <typename T, typename OUT_T, int MODE, int NT, int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)[FM][FN],
+                                                int64_t bidx, int m0, int n0, int wrow0,
+                                                int wcol0, bool diag_tile, unsigned char* smem) {
+  constexpr int ELD = epi_ld<BN>();
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x, lane = tid & 63, lrow = lane & 31, lk = lane >> 5;
+  OUT_T* tile = reinterpret_cast<OUT_T*>(smem);
+  const T* D = g.d ? reinterpret_cast<const T*>(g.d) + bidx * g.sd : nullptr;
+  OUT_T* C = g.c ? reinterpret_cast<OUT_T*>(g.c) + bidx * g.sc : nullptr;
+  OUT_T* CT = g.ct ? reinterpret_cast<OUT_T*>(g.ct) + bidx * g.sct : nullptr;
+  OUT_T* CD = g.c_diag ? reinterpret_cast<OUT_T*>(g.c_diag) + bidx * g.sc : nullptr;
+  const bool vec_rows = (g.ldd % 8 == 0) && (g.ldc % 8 == 0) && (g.sc % 8 == 0) &&
+                        (g.sd % 8 == 0);
+  // Every wave is done with the pipeline's LDS before the tile overwrites it.
+  __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0) lgkmcnt(0)
+  __syncthreads();
+  if (D) {
+    for (int q = tid; q < BM * BN / 8; q += NT) {
+      const int r = q / (BN / 8), c8 = (q % (BN / 8)) * 8;
+      const int gr = m0 + r, gc = n0 + c8;
+      T* dst = reinterpret_cast<T*>(tile) + r * ELD + c8;
+      if (gr < g.m_lim && gc + 8 <= g.n_lim && vec_rows) {
+        *reinterpret_cast<u4*>(dst) = *reinterpret_cast<const u4*>(D + (int64_t)gr * g.ldd + gc);
+      } else {
+        for (int e = 0; e < 8; ++e)
+          dst[e] = (gr < g.m_lim && gc + e < g.n_lim) ? D[(int64_t)gr * g.ldd + gc + e] : (T)0.f;
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = wcol0 + j * 32 + lrow;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+        float x = g.alpha * acc[i][j][e];
+        if (D) x += g.beta * (float)reinterpret_cast<const T*>(tile)[row * ELD + col];
+        tile[row * ELD + col] = round_out<OUT_T, MODE>(x);
+      }
+    }
+  __syncthreads();
+  // Straight stores: rows of the tile (on a diagonal tile, columns >= row).
+  if (C || CD) {
+    for (int q = tid; q < BM * BN / 8; q += NT) {
+      const int r = q / (BN / 8), c8 = (q % (BN / 8)) * 8;
+      const int gr = m0 + r, gc = n0 + c8;
+      if (gr >= g.m_lim || gc >= g.n_lim) continue;
+      const OUT_T* src = tile + r * ELD + c8;
+      const bool whole = gc + 8 <= g.n_lim && !(diag_tile && c8 < r) && vec_rows;
+      if (whole && !(CD && gr >= gc && gr < gc + 8)) {
+        const u4 v = *reinterpret_cast<const u4*>(src);
+        if (C) *reinterpret_cast<u4*>(C + (int64_t)gr * g.ldc + gc) = v;
+        if (CD) *reinterpret_cast<u4*>(CD + (int64_t)gr * g.ldc + gc) = v;
+      } else {
+        for (int e = 0; e < 8; ++e) {
+          const int c = gc + e;
+          if (c >= g.n_lim || (diag_tile && c8 + e < r)) continue;
+          if (C) C[(int64_t)gr * g.ldc + c] = src[e];
+          if (CD) CD[(int64_t)gr * g.ldc + c] = (OUT_T)((float)src[e] + (gr == c ? g.diag_shift : 0.f));
+        }
+      }
+    }
+  }
+  // Transposed / mirrored stores: column c of the tile becomes row n0 + c.
+  // Lane -> (8 columns, 8 row blocks of 8) so that 8 lanes write 128 contiguous bytes.
+  OUT_T* TT = CT ? CT : nullptr;
+  if (TT) {
+    const int64_t ldt = g.ct ? g.ldct : g.ldc;
+    for (int q = tid; q < BM * BN / 8; q += NT) {
+      const int c = (q / 64) % (BN / 8) * 8 + (q & 7);
+      const int r8 = ((q & 63) >> 3) * 8 + (q / (64 * (BN / 8))) * 64;
+      if (r8 >= BM) continue;
+      const int gr = m0 + r8, gc = n0 + c;
+      if (gc >= g.n_lim || gr >= g.m_lim) continue;
+      OUT_T v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = tile[(r8 + e) * ELD + c];
+      const bool mirror_skip_any = diag_tile && r8 + 7 >= c;
+      if (!mirror_skip_any && gr + 8 <= g.m_lim && ldt % 8 == 0 && g.sct % 8 == 0 &&
+          (reinterpret_cast<uintptr_t>(TT) & 15) == 0) {
+        u4 w;
+        __builtin_memcpy(&w, v, 16);
+        *reinterpret_cast<u4*>(TT + (int64_t)gc * ldt + gr) = w;
+        if (g.sym && CD) {
+          OUT_T vd[8];
+          for (int e = 0; e < 8; ++e) vd[e] = v[e];  // off-diagonal: no shift
+          __builtin_memcpy(&w, vd, 16);
+          *reinterpret_cast<u4*>(CD + (int64_t)gc * g.ldc + gr) = w;
+        }
+      } else {
+        for (int e = 0; e < 8; ++e) {
+          const int r = r8 + e;
+          if (m0 + r >= g.m_lim || (diag_tile && r >= c)) continue;
+          TT[(int64_t)gc * ldt + m0 + r] = v[e];
+          if (g.sym && CD) CD[(int64_t)gc * g.ldc + m0 + r] = v[e];
+        }
+      }
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  // s_waitcnt vmcnt(N) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+template <typename T, typename OUT_T, int MODE, typename CFG>
+__global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs g, int batch) {
+  constexpr int PBM = CFG::BM, PBN = CFG::BN, PWN = CFG::WN, PSTAGES = CFG::STAGES;
+  constexpr int PSTAGE_ELEMS = CFG::stage_elems, LA = CFG::loads_a, LB = CFG::loads_b;
+  constexpr int WTM = PBM / CFG::WM, WTN = PBN / PWN;  // wave tile
+  constexpr int FM = WTM / 32, FN = WTN / 32;      // 32x32 fragments
+  using V = typename Mfma<T>::vec;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  T* lds = reinterpret_cast<T*>(smem);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / PWN, wn = wave % PWN;
+
+  // XCD-aware order: the hardware deals workgroup w to XCD w % 8; give each
+  // XCD a contiguous range of logical tiles so that its L2 sees reuse.
+  const int tiles = g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
+  const int total = tiles * batch;
+  int w = blockIdx.x;
+  {
+    const int per = total / 8, extra = total % 8, x = w % 8, i = w / 8;
+    w = x * per + min(x, extra) + i;
+  }
+  const int64_t bidx = w / tiles;
+  const int t = w - (int)bidx * tiles;
+  int tm, tn;
+  if (g.sym) {
+    tri_tile(t, tm, tn);
+  } else {
+    const int group = 8 * g.tiles_n;
+    const int first = (t / group) * 8;
+    const int gm = min(g.tiles_m - first, 8);
+    tm = first + (t % group) % gm;
+    tn = (t % group) / gm;
+  }
+  const int m0 = tm * PBM, n0 = tn * PBN;
+  const T* A = reinterpret_cast<const T*>(g.a) + bidx * g.sa;
+  const T* B = reinterpret_cast<const T*>(g.b) + bidx * g.sb;
+
+  // Per-thread load slots: slot j of wave w covers LDS chunks
+  // [(w * L + j) * 64, +64) of the operand's stage area (L loads per thread).
+  const T* a_src[LA];
+  const T* b_src[LB];
+#pragma unroll
+  for (int j = 0; j < LA; ++j) {
+    const int pos = (wave * LA + j) * 64 + lane;  // 16-byte chunk index
+    const int row = pos >> 2, logical = (pos & 3) ^ ((row >> 2) & 3);
+    a_src[j] = A + (int64_t)min(m0 + row, g.m - 1) * g.lda + logical * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < LB; ++j) {
+    const int pos = (wave * LB + j) * 64 + lane;
+    const int row = pos >> 2, logical = (pos & 3) ^ ((row >> 2) & 3);
+    b_src[j] = B + (int64_t)min(n0 + row, g.n - 1) * g.ldb + logical * 8;
+  }
+  auto issue = [&](int kt) {
+    T* stage = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
+    const int k0 = kt * PBK;
+#pragma unroll
+    for (int j = 0; j < LA; ++j)  // wave-uniform LDS destination: lane i lands at +16 i bytes
+      __builtin_amdgcn_global_load_lds((const void*)(a_src[j] + k0),
+                                       (lds_ptr_t)(stage + (wave * LA + j) * 512), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < LB; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(b_src[j] + k0),
+                                       (lds_ptr_t)(stage + PBM * PBK + (wave * LB + j) * 512), 16,
+                                       0, 0);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int kt_count = g.k / PBK;
+#pragma unroll
+  for (int s = 0; s < PSTAGES - 1; ++s)
+    if (s < kt_count) issue(s);
+  const int lrow = lane & 31, lk = lane >> 5;
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const int ahead = min(PSTAGES - 2, kt_count - 1 - kt);  // stages issued after kt
+    static_assert(PSTAGES >= 2 && PSTAGES <= 4, "waits cover 0..2 stages ahead");
+    if (ahead >= 2) wait_vm_lgkm0<2 * (LA + LB)>();
+    else if (ahead == 1) wait_vm_lgkm0<LA + LB>();
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    if (kt + PSTAGES - 1 < kt_count) issue(kt + PSTAGES - 1);
+    const T* As = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
+    const T* Bs = As + PBM * PBK;
+#pragma unroll
+    for (int ks = 0; ks < PBK / 16; ++ks) {
+      V af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const V*>(As + plds_off(wm * WTM + i * 32 + lrow, 2 * ks + lk));
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const V*>(Bs + plds_off(wn * WTN + j * 32 + lrow, 2 * ks + lk));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<T>::run(af[i], bfr[j], acc[i][j]);
+    }
+  }
+
+  staged_epilogue<T, OUT_T, MODE, CFG::threads, PBM, PBN, FM, FN>(
+      g, acc, bidx, m0, n0, wm * WTM, wn * WTN, g.sym && tm == tn, smem);
+}
+
+// ---- hand-scheduled 256x256 kernel -----------------------------------------------
+//
+// 4 waves of 128x128 (16 AGPR accumulators each, one wave per SIMD), BK = 32,
+// 4-stage LDS ring refilled 4 stages ahead. Fragment registers are double
+// buffered: while the 16 MFMAs of one 16-deep k step run, the 8 fragment reads
+// of the next step (and, in the second half, the 8 direct-to-LDS loads of a
+// future stage) are interleaved between them by sched_group_barrier. The one
+// barrier per stage sits between the two halves, after which the stage just
+// consumed is refilled; its reads have completed (lgkmcnt(0)) in every wave.
+
+constexpr int HBM_ = 256, HSTAGES = 4;
+constexpr int HSTAGE_ELEMS = 2 * HBM_ * PBK;
+constexpr int HLOADS = HBM_ * PBK / 8 / 256;  // 4 per operand per thread
+
+template <typename T, typename OUT_T, int MODE>
+__global__ __launch_bounds__(256, 1) void gemm_nt_sched_kernel(GemmArgs g, int batch) {
+  constexpr int WT = 128, F = 4;
+  using V = typename Mfma<T>::vec;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  T* lds = reinterpret_cast<T*>(smem);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int tiles = g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
+  const int total = tiles * batch;
+  int w = blockIdx.x;
+  {
+    const int per = total / 8, extra = total % 8, x = w % 8, i = w / 8;
+    w = x * per + min(x, extra) + i;
+  }
+  const int64_t bidx = w / tiles;
+  const int t = w - (int)bidx * tiles;
+  int tm, tn;
+  if (g.sym) {
+    tri_tile(t, tm, tn);
+  } else {
+    const int group = 8 * g.tiles_n;
+    const int first = (t / group) * 8;
+    const int gm = min(g.tiles_m - first, 8);
+    tm = first + (t % group) % gm;
+    tn = (t % group) / gm;
+  }
+  const int m0 = tm * HBM_, n0 = tn * HBM_;
+  const T* A = reinterpret_cast<const T*>(g.a) + bidx * g.sa;
+  const T* B = reinterpret_cast<const T*>(g.b) + bidx * g.sb;
+  const T* a_src[HLOADS];
+  const T* b_src[HLOADS];
+#pragma unroll
+  for (int j = 0; j < HLOADS; ++j) {
+    const int pos = (wave * HLOADS + j) * 64 + lane;
+    const int row = pos >> 2, logical = (pos & 3) ^ ((row >> 2) & 3);
+    a_src[j] = A + (int64_t)min(m0 + row, g.m - 1) * g.lda + logical * 8;
+    b_src[j] = B + (int64_t)min(n0 + row, g.n - 1) * g.ldb + logical * 8;
+  }
+  auto issue = [&](int kt) {
+    T* stage = lds + (kt % HSTAGES) * HSTAGE_ELEMS;
+    const int k0 = kt * PBK;
+#pragma unroll
+    for (int j = 0; j < HLOADS; ++j) {
+      __builtin_amdgcn_global_load_lds((const void*)(a_src[j] + k0),
+                                       (lds_ptr_t)(stage + (wave * HLOADS + j) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(b_src[j] + k0),
+                                       (lds_ptr_t)(stage + HBM_ * PBK + (wave * HLOADS + j) * 512),
+                                       16, 0, 0);
+    }
+  };
+  const int lrow = lane & 31, lk = lane >> 5;
+  int a_off[F], b_off[F][2];
+#pragma unroll
+  for (int i = 0; i < F; ++i) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      b_off[i][ks] = HBM_ * PBK + plds_off(wn * WT + i * 32 + lrow, 2 * ks + lk);
+    }
+    a_off[i] = plds_off(wm * WT + i * 32 + lrow, lk);  // ks = 0; ks = 1 is chunk ^ 2
+  }
+  auto read = [&](V (&af)[F], V (&bf)[F], const T* stage, int ks) {
+#pragma unroll
+    for (int i = 0; i < F; ++i) {
+      const int off = ks ? plds_off(wm * WT + i * 32 + lrow, 2 + lk) : a_off[i];
+      af[i] = *reinterpret_cast<const V*>(stage + off);
+    }
+#pragma unroll
+    for (int j = 0; j < F; ++j) bf[j] = *reinterpret_cast<const V*>(stage + b_off[j][ks]);
+  };
+
+  f32x16 acc[F][F];
+#pragma unroll
+  for (int i = 0; i < F; ++i)
+#pragma unroll
+    for (int j = 0; j < F; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int kt_count = g.k / PBK;
+  for (int s = 0; s < HSTAGES; ++s)
+    if (s < kt_count) issue(s);
+  // Stage 0 ready: allow the loads of stages 1..3 to stay in flight.
+  if (kt_count >= 4) wait_vm_lgkm0<6 * HLOADS>();
+  else if (kt_count == 3) wait_vm_lgkm0<4 * HLOADS>();
+  else if (kt_count == 2) wait_vm_lgkm0<2 * HLOADS>();
+  else wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  V a_cur[F], b_cur[F], a_nxt[F], b_nxt[F];
+  read(a_cur, b_cur, lds, 0);
+
+  for (int kt = 0; kt < kt_count; ++kt) {
+    const T* stage = lds + (kt % HSTAGES) * HSTAGE_ELEMS;
+    // First half: MFMAs of (kt, k step 0), reads of (kt, k step 1).
+    read(a_nxt, b_nxt, stage, 1);
+#pragma unroll
+    for (int i = 0; i < F; ++i)
+#pragma unroll
+      for (int j = 0; j < F; ++j) acc[i][j] = Mfma<T>::run(a_cur[i], b_cur[j], acc[i][j]);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    // Stage kt + 1 complete in every wave, stage kt fully read: meet, refill.
+    const int ahead = min(2, kt_count - 2 - kt);  // stages after kt + 1 still loading
+    if (ahead >= 2) wait_vm_lgkm0<4 * HLOADS>();
+    else if (ahead == 1) wait_vm_lgkm0<2 * HLOADS>();
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const bool refill = kt + HSTAGES < kt_count;
+    if (refill) issue(kt + HSTAGES);
+    const T* next_stage = lds + ((kt + 1) % HSTAGES) * HSTAGE_ELEMS;
+    // Second half: MFMAs of (kt, k step 1), reads of (kt + 1, k step 0) (on the
+    // last stage these read a stale, in-bounds stage and are never used).
+    read(a_cur, b_cur, next_stage, 0);
+#pragma unroll
+    for (int i = 0; i < F; ++i)
+#pragma unroll
+      for (int j = 0; j < F; ++j) acc[i][j] = Mfma<T>::run(a_nxt[i], b_nxt[j], acc[i][j]);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  staged_epilogue<T, OUT_T, MODE, 256, HBM_, HBM_, F, F>(g, acc, bidx, m0, n0, wm * WT, wn * WT,
+                                                        g.sym && tm == tn, smem);
+}
+
+template <typename T, typename OUT_T, int MODE>
+int launch_sched(const Problem& p, hipStream_t stream) {
+  GemmArgs g = p.g;
+  g.ct_vec = !g.ct || (g.ldct % 4 == 0 && g.sct % 4 == 0 &&
+                       (reinterpret_cast<uintptr_t>(g.ct) & 7) == 0);
+  if (g.c_diag && g.sym) g.ct_vec = g.ct_vec && g.ldc % 4 == 0 && g.sc % 4 == 0;
+  constexpr size_t pipe_bytes = (size_t)HSTAGES * HSTAGE_ELEMS * 2;
+  constexpr size_t lds_bytes = pipe_bytes > epi_lds_bytes<HBM_, HBM_>() ? pipe_bytes
+                                                                     : epi_lds_bytes<HBM_, HBM_>();
+  auto kern = gemm_nt_sched_kernel<T, OUT_T, MODE>;
+  static std::once_flag once;
+  static hipError_t attr_rc = hipSuccess;
+  std::call_once(once, [&] {
+    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+  });
+  if (attr_rc != hipSuccess) {
+    set_error("gemm: hipFuncSetAttribute failed: %s", hipGetErrorString(attr_rc));
+    return kHipError;
+  }
+  g.tiles_m = (g.m + HBM_ - 1) / HBM_;
+  g.tiles_n = (g.n + HBM_ - 1) / HBM_;
+  if (g.sym && g.m != g.n) {
+    set_error("gemm: symmetric mode needs a square output");
+    return kInvalid;
+  }
+  const int64_t tiles = g.sym ? (int64_t)g.tiles_m * (g.tiles_m + 1) / 2
+                              : (int64_t)g.tiles_m * g.tiles_n;
+  if (tiles * p.batch > INT32_MAX) {
+    set_error("gemm: grid too large");
+    return kInvalid;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * p.batch)), dim3(256), lds_bytes, stream, g,
+                     (int)p.batch);
+  return check_launch("gemm_nt_sched");
+}
+
 // ---- launch configuration ----------------------------------------------------
 
-struct Problem {
-  int elem;  // kF16 / kBF16
-  int out_mode;
-  int64_t batch;
-  GemmArgs g;
-};
 
 template <typename T, typename OUT_T, int BM, int BN, int WM, int WN, int MODE>
 int launch_cfg(const Problem& p, hipStream_t stream) {
@@ -308,12 +767,72 @@ int launch_cfg(const Problem& p, hipStream_t stream) {
   return check_launch("gemm_nt");
 }
 
+template <typename T, typename OUT_T, int MODE, typename CFG>
+int launch_pipe(const Problem& p, hipStream_t stream) {
+  GemmArgs g = p.g;
+  g.ct_vec = !g.ct || (g.ldct % 4 == 0 && g.sct % 4 == 0 &&
+                       (reinterpret_cast<uintptr_t>(g.ct) & 7) == 0);
+  if (g.c_diag && g.sym) g.ct_vec = g.ct_vec && g.ldc % 4 == 0 && g.sc % 4 == 0;
+  constexpr size_t lds_bytes = CFG::lds_bytes > epi_lds_bytes<CFG::BM, CFG::BN>()
+                                  ? CFG::lds_bytes : epi_lds_bytes<CFG::BM, CFG::BN>();
+  auto kern = gemm_nt_pipe_kernel<T, OUT_T, MODE, CFG>;
+  static std::once_flag once;
+  static hipError_t attr_rc = hipSuccess;
+  std::call_once(once, [&] {
+    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+  });
+  if (attr_rc != hipSuccess) {
+    set_error("gemm: hipFuncSetAttribute failed: %s", hipGetErrorString(attr_rc));
+    return kHipError;
+  }
+  g.tiles_m = (g.m + CFG::BM - 1) / CFG::BM;
+  g.tiles_n = (g.n + CFG::BN - 1) / CFG::BN;
+  if (g.sym && (g.m != g.n || CFG::BM != CFG::BN)) {
+    set_error("gemm: symmetric mode needs a square output and square tiles");
+    return kInvalid;
+  }
+  const int64_t tiles = g.sym ? (int64_t)g.tiles_m * (g.tiles_m + 1) / 2
+                              : (int64_t)g.tiles_m * g.tiles_n;
+  if (tiles * p.batch > INT32_MAX) {
+    set_error("gemm: grid too large");
+    return kInvalid;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * p.batch)), dim3(CFG::threads), lds_bytes, stream,
+                     g, (int)p.batch);
+  return check_launch("gemm_nt_pipe");
+}
+
 template <typename T, typename OUT_T, int MODE>
 int launch_typed(const Problem& p, hipStream_t stream) {
   // Large outputs: 128x128 tiles (4 waves of 64x64); small ones 64x64 tiles
   // so that a batch of small blocks still fills the 256 CUs.
   const int64_t big_tiles = p.batch * ((p.g.m + 127) / 128) * ((p.g.n + 127) / 128) /
                             (p.g.sym ? 2 : 1);
+  const int64_t huge_tiles = p.batch * ((p.g.m + 255) / 256) * ((p.g.n + 255) / 256) /
+                             (p.g.sym ? 2 : 1);
+  if (p.g.k % PBK == 0 && huge_tiles >= 256) {
+// Tile configuration of the large products; 4 (256x256 tiles, 16 waves of
+// 64x64) measured fastest on the Llama-3-8B Newton-Schulz shapes.
+#ifndef DIONW_PIPE_CFG
+#define DIONW_PIPE_CFG 4
+#endif
+#if DIONW_PIPE_CFG == 0
+    return launch_pipe<T, OUT_T, MODE, PipeCfg<256, 256, 2, 4, 4>>(p, stream);
+#elif DIONW_PIPE_CFG == 1
+    return launch_pipe<T, OUT_T, MODE, PipeCfg<256, 256, 2, 4, 3>>(p, stream);
+#elif DIONW_PIPE_CFG == 2
+    return launch_pipe<T, OUT_T, MODE, PipeCfg<128, 128, 2, 2, 4>>(p, stream);
+#elif DIONW_PIPE_CFG == 3
+    return launch_pipe<T, OUT_T, MODE, PipeCfg<128, 128, 2, 2, 3>>(p, stream);
+#elif DIONW_PIPE_CFG == 4
+    return launch_pipe<T, OUT_T, MODE, PipeCfg<256, 256, 4, 4, 4>>(p, stream);
+#elif DIONW_PIPE_CFG == 5
+    return launch_pipe<T, OUT_T, MODE, PipeCfg<128, 128, 2, 2, 2>>(p, stream);
+#elif DIONW_PIPE_CFG == 6
+    return launch_sched<T, OUT_T, MODE>(p, stream);
+#endif
+  }
   if (big_tiles >= 512) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
   return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
 }

@@ -98,7 +98,9 @@ def test_accumulate_copy_decay(nesterov: bool) -> None:
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize(("batch", "m", "n", "k"), [(1, 64, 64, 64), (3, 100, 72, 136),
-                                                    (2, 256, 512, 1024), (5, 352, 352, 2048)])
+                                                    (2, 256, 512, 1024), (5, 352, 352, 2048),
+                                                    # large enough for the pipelined 256x256 kernel
+                                                    (20, 1024, 1024, 512), (20, 1000, 1032, 512)])
 def test_gemm_nt_matches_fp32(dtype: torch.dtype, batch: int, m: int, n: int, k: int) -> None:
     g = _gen(3)
     a = torch.randn(batch, m, k, generator=g).to(dtype)
@@ -118,6 +120,17 @@ def test_gemm_nt_matches_fp32(dtype: torch.dtype, batch: int, m: int, n: int, k:
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(3, 64, 256), (3, 128, 128), (96, 160), (2, 520, 1032)])
 def test_symmetric_products(dtype: torch.dtype, shape: tuple[int, ...]) -> None:
+    _check_symmetric(dtype, shape)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_symmetric_products_pipelined(dtype: torch.dtype) -> None:
+    """Batches large enough for the pipelined 256x256 kernel, ragged 1000 rows."""
+    _check_symmetric(dtype, (40, 1024, 1024))
+    _check_symmetric(dtype, (48, 1000, 1024))
+
+
+def _check_symmetric(dtype: torch.dtype, shape: tuple[int, ...]) -> None:
     g = _gen(4)
     x = (torch.randn(*shape, generator=g) / shape[-1] ** 0.5).to(dtype)
     gram = _kernels.ns_line_1(x.to(DEV))
