@@ -93,6 +93,8 @@ class Timeline:
             if name == "dionw_newton_schulz":
                 kind, batch, r_real, c_real = a[0], a[1], a[6], a[7]
                 entry["flops"] += batch * ns_flops(kind, r_real, c_real)
+                # MFMA product launches of the call: 18 for the Gram iteration, 15 otherwise.
+                entry["launches"] = entry.get("launches", 0) + (18 if kind == 0 and c_real > r_real else 15)
             elif name == "dionw_accumulate_scores":
                 count, rows, cols = a[1], a[2], a[3]
                 entry["bytes"] += 12.0 * count * rows * cols
@@ -163,22 +165,65 @@ def cpu_baseline(spec, fraction: float, threads: int) -> dict:
         dion_ref.adamw(ap, ag, am, av, float(step), lr=3e-4, beta1=0.9, beta2=0.95,
                        weight_decay=0.05, eps=1e-8)
 
+    sample_layers = 3
     t0 = time.perf_counter()
-    one_layer(1)
-    per_layer = time.perf_counter() - t0
+    for step in range(sample_layers):
+        one_layer(step + 1)
+    per_layer = (time.perf_counter() - t0) / sample_layers
     return {
         "value": per_layer * spec["layers"] * 1e3,
         "unit": "ms/step (extrapolated)",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle (torch CPU restatement) on 1 of {spec['layers']} layers' Dion blocks "
-                  f"+ 1/{spec['layers']} of the AdamW elements, x{spec['layers']}",
-        "sample_seconds": round(per_layer, 2),
+        "sample": f"oracle (torch CPU restatement): one decoder layer's Dion blocks + "
+                  f"1/{spec['layers']} of the AdamW elements, stepped {sample_layers} times; "
+                  f"mean per layer x{spec['layers']} layers",
+        "sample_seconds": round(per_layer * sample_layers, 2),
     }
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def traffic_bytes():
+    """HBM bytes per launch of the dominant product, from the committed
+    FETCH_SIZE / WRITE_SIZE measurement (``--probe`` under rocprofv3 --pmc), or None."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+        return data["gemm_sym_r3584"]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def probe() -> int:
+    """One launch of each kernel whose traffic is measured, plus a copy of known
+    size for calibrating the counters (run under ``rocprofv3 --pmc``)."""
+    import torch
+
+    from dionw_amd import _kernels, _lib
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(256 * 2**20, device=dev)  # 1 GiB of float32
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    g = torch.randn(18, 3584, 3584, device=dev).half()
+    z = torch.empty_like(g)
+    _kernels.gemm_nt(g, g, d=g, alpha=0.5, beta=-1.5, out=z, symmetric=True)
+    grads = [torch.randn(14336, 4096, device=dev) * 1e-3 for _ in range(18)]
+    mom = torch.zeros(18 * 14336, 4096, device=dev)
+    scores = torch.empty(18 * 14336, device=dev)
+    rowsq = torch.empty_like(scores)
+    _lib.call("dionw_accumulate_scores", _lib.ptr_array(grads), 18, 14336, 4096, mom.data_ptr(),
+              scores.data_ptr(), rowsq.data_ptr(), _lib.stream_handle(dev))
+    torch.cuda.synchronize()
+    print("probe done: copy 1 GiB, gemm_nt sym 18x3584^2 k=3584, accumulate 18x14336x4096")
+    return 0
 
 
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--probe", action="store_true",
+                        help="run the counter-calibration launches and exit")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=5)
     parser.add_argument("--warmup", type=int, default=2)
@@ -186,6 +231,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--instrumented-steps", type=int, default=2)
     args = parser.parse_args()
+    if args.probe:
+        return probe()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the optimizer step is single-device); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
@@ -272,8 +319,9 @@ def main() -> int:
             "peak": PEAK_MFMA_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(ns_tflops / PEAK_MFMA_TFLOPS, 4),
-            "traffic": None,
-            "avg_launch_us": round(ns["ms"] * 1e3 / max(ns.get("calls", 0), 1), 1),
+            "traffic": traffic_bytes(),
+            "avg_launch_us": round(ns["ms"] * 1e3 / max(ns.get("launches", 0), 1), 1),
+            "launches_per_step": ns.get("launches", 0) // div,
         },
         "cpu_baseline": cpu,
     }
