@@ -136,6 +136,88 @@ def build_llama(torch, dev, spec, fraction):
     return groups, n_params
 
 
+def build_gpt2(torch, dev):
+    """GPT-2 small. Every linear is Dion with fraction 0.25 and
+    selection_min_dim 1024, so with their 768-wide sides all update every row;
+    LayerNorm weights/biases, linear biases, wte 50257x768 and wpe 1024x768 take AdamW."""
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def param(*shape):
+        p = torch.nn.Parameter(torch.empty(*shape, device=dev).normal_(0.0, 0.02, generator=g))
+        p.grad = torch.empty_like(p).normal_(0.0, 1e-3, generator=g)
+        return p
+
+    matrices, vectors = [], []
+    for _ in range(GPT2["layers"]):
+        for _, rows, cols in GPT2["matrices"]:
+            matrices.append(param(rows, cols))
+            vectors.append(param(rows))                      # linear bias
+        vectors.extend(param(768) for _ in range(4))         # two LayerNorms
+    vectors.extend([param(768), param(768)])                 # final LayerNorm
+    embed = [param(50257, 768), param(1024, 768)]
+    groups = [
+        {"params": embed + vectors, "dion_route": "adamw", "weight_decay": 0.0},
+        {"params": matrices, "dion_route": "matrix", "fraction": 1.0},
+    ]
+    return groups, sum(p.numel() for grp in groups for p in grp["params"])
+
+
+def build_moe(torch, dev):
+    """64 experts with fp32 gate/up 1408x2048 and down 2048x1408
+    (separate 2-D parameters), gradients 1e-3 * Student-t(df=3)."""
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def student_t(*shape):
+        z = torch.empty(*shape, device=dev).normal_(generator=g)
+        chi2 = sum(torch.empty(*shape, device=dev).normal_(generator=g) ** 2 for _ in range(3))
+        return z / torch.sqrt(chi2 / 3.0) * 1e-3
+
+    def param(*shape):
+        p = torch.nn.Parameter(torch.empty(*shape, device=dev).normal_(0.0, 0.02, generator=g))
+        p.grad = student_t(*shape)
+        return p
+
+    experts = []
+    for _ in range(64):
+        experts += [param(1408, 2048), param(1408, 2048), param(2048, 1408)]
+    return experts, sum(p.numel() for p in experts)
+
+
+def gram_ns_bench(torch, steps: int, warmup: int) -> dict:
+    """standalone Gram Newton-Schulz on 16 bf16 blocks 1024x4096,
+    entries N(0,1) pre-normalized by their Frobenius norm, 5 iterations."""
+    from dionw_amd.newton_schulz import NewtonSchulz, newton_schulz_fn
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.empty(16, 1024, 4096, device=dev).normal_(generator=g)
+    x = (x / torch.linalg.vector_norm(x, dim=(-2, -1), keepdim=True)).bfloat16()
+    fn = newton_schulz_fn(NewtonSchulz.GRAM)
+    for _ in range(warmup):
+        fn(x, 1e-8)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        fn(x, 1e-8)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = 16 * ns_flops(0, 1024, 4096)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "Gram Newton-Schulz ms, 16 x 1024x4096 bf16 (config 2)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 MFMA (bf16 input)", "data": "synthetic",
+        "config": {"workload": "gram-ns: 16 blocks 1024x4096, 5 iterations, restart at 2"},
+        "gram_ns_tflops": round(tflops, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_MFMA_TFLOPS, 4),
+                     "traffic": None},
+    }
+
+
 def cpu_baseline(spec, fraction: float, threads: int) -> dict:
     """The CPU oracle on one decoder layer's Dion blocks plus 1/layers of the
     AdamW elements, scaled by the layer count (labelled extrapolated)."""
@@ -227,7 +309,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=5)
     parser.add_argument("--warmup", type=int, default=2)
-    parser.add_argument("--config", default="llama3-8b", choices=["llama3-8b", "gpt2-small"])
+    parser.add_argument("--config", default="llama3-8b",
+                        choices=["llama3-8b", "gpt2-small", "gram-ns", "moe", "moe-muon"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--instrumented-steps", type=int, default=2)
     args = parser.parse_args()
@@ -243,13 +326,28 @@ def main() -> int:
     import dionw_amd
     from dionw_amd import _lib
 
+    if args.config == "gram-ns":
+        print(json.dumps(gram_ns_bench(torch, args.steps, args.warmup)), flush=True)
+        return 0
     dev = torch.device("cuda:0")
     spec = LLAMA if args.config == "llama3-8b" else GPT2
     fraction = 0.25
     print(f"[bench] building {args.config} parameters", file=sys.stderr, flush=True)
-    groups, n_params = build_llama(torch, dev, spec, fraction)
+    kwargs = {}
+    if args.config == "llama3-8b":
+        groups, n_params = build_llama(torch, dev, spec, fraction)
+    elif args.config == "gpt2-small":
+        groups, n_params = build_gpt2(torch, dev)
+    else:
+        experts, n_params = build_moe(torch, dev)
+        if args.config == "moe":
+            groups = [{"params": experts, "dion_route": "matrix", "fraction": fraction}]
+            kwargs["ema"] = dionw_amd.EMAConfig(decay=0.9999, update_every_n_steps=1)
+        else:
+            groups = [{"params": experts, "dion_route": "matrix", "fraction": 1.0}]
+            kwargs["matrix_update"] = dionw_amd.MUON_UPDATE
     opt = dionw_amd.Dion(groups, lr=3e-4, weight_decay=0.05, momentum=0.95, muon_beta2=0.95,
-                         betas=(0.9, 0.95), eps=1e-8)
+                         betas=(0.9, 0.95), eps=1e-8, **kwargs)
     torch.cuda.synchronize()
     print(f"[bench] {n_params / 1e9:.2f} G params; warmup {args.warmup}", file=sys.stderr,
           flush=True)
@@ -285,13 +383,17 @@ def main() -> int:
     print(f"[bench] phases {json.dumps(phases)}", file=sys.stderr, flush=True)
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.config == "llama3-8b":
         print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(spec, fraction, threads=min(os.cpu_count() or 1, 16))
 
     line = {
-        "metric": "Dion step ms at Llama-3-8B shapes" if args.config == "llama3-8b"
-        else "Dion step ms at GPT-2-small shapes",
+        "metric": {
+            "llama3-8b": "Dion step ms at Llama-3-8B shapes",
+            "gpt2-small": "Dion step ms at GPT-2-small shapes (config 3)",
+            "moe": "Dion step ms, MoE 64 experts + GPU EMA (config 5a)",
+            "moe-muon": "Muon step ms, MoE 64 experts (config 5b)",
+        }[args.config],
         "value": round(ms, 3),
         "unit": "ms",
         "n_gpus": 1,
@@ -304,8 +406,16 @@ def main() -> int:
         "dtype": "f32 state, f16/bf16 MFMA Newton-Schulz",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.config}: full Dion step (Dion f={fraction} on every linear, "
-                        "AdamW on embeddings/lm_head/norms), fp32 params resident in HBM",
+            "workload": {
+                "llama3-8b": f"llama3-8b: full Dion step (Dion f={fraction} on every linear, "
+                             "AdamW on embeddings/lm_head/norms), fp32 params resident in HBM",
+                "gpt2-small": "gpt2-small: Dion on every linear (all rows: min side 768 < 1024), "
+                              "AdamW on LayerNorms, biases, wte, wpe",
+                "moe": "moe: 64 experts gate/up 1408x2048 + down 2048x1408, Dion f=0.25, "
+                       "GPU EMA 0.9999 every step, Student-t(3) gradients",
+                "moe-muon": "moe-muon: the same experts with MUON_UPDATE (Keller bf16, Nesterov, "
+                            "every row)",
+            }[args.config],
             "params": n_params,
         },
         "gram_ns_tflops": round(ns_tflops, 1),

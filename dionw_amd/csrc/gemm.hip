@@ -554,6 +554,23 @@ constexpr int HBM_ = 256, HSTAGES = 4;
 constexpr int HSTAGE_ELEMS = 2 * HBM_ * PBK;
 constexpr int HLOADS = HBM_ * PBK / 8 / 256;  // 4 per operand per thread
 
+// Instruction order of one half step (16 MFMAs, 8 fragment reads).
+#ifndef DIONW_SCHED_ORDER
+#define DIONW_SCHED_ORDER 1
+#endif
+__device__ __forceinline__ void sched_half() {
+#if DIONW_SCHED_ORDER == 0
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+  }
+#else
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the next step's 8 reads first
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+#endif
+}
+
 template <typename T, typename OUT_T, int MODE>
 __global__ __launch_bounds__(256, 1) void gemm_nt_sched_kernel(GemmArgs g, int batch) {
   constexpr int WT = 128, F = 4;
@@ -654,11 +671,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_sched_kernel(GemmArgs g, int b
     for (int i = 0; i < F; ++i)
 #pragma unroll
       for (int j = 0; j < F; ++j) acc[i][j] = Mfma<T>::run(a_cur[i], b_cur[j], acc[i][j]);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+    sched_half();
     // Stage kt + 1 complete in every wave, stage kt fully read: meet, refill.
     const int ahead = min(2, kt_count - 2 - kt);  // stages after kt + 1 still loading
     if (ahead >= 2) wait_vm_lgkm0<4 * HLOADS>();
@@ -676,11 +689,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_sched_kernel(GemmArgs g, int b
     for (int i = 0; i < F; ++i)
 #pragma unroll
       for (int j = 0; j < F; ++j) acc[i][j] = Mfma<T>::run(a_nxt[i], b_nxt[j], acc[i][j]);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+    sched_half();
     __builtin_amdgcn_sched_barrier(0);
   }
 

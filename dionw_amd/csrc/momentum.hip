@@ -18,6 +18,7 @@
 
 #include "common.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace dionw {
@@ -374,56 +375,69 @@ int dionw_prepare_ns_input(const float* const* grads, int32_t count, float* mome
   DIONW_REQUIRE(!full || k == rows, "prepare_ns_input: every-row mode needs k == rows");
   DIONW_REQUIRE(elem == kF16 || elem == kBF16 || elem == kF32, "prepare_ns_input: bad elem %d",
                 elem);
-  if (blocks == 0) return kOk;
-  PrepArgs a{};
-  a.momentum = momentum;
-  a.idx = idx;
-  a.den = den;
-  a.out_r = out_rowmajor;
-  a.out_t = out_transposed;
-  a.rows = rows;
-  a.cols = cols;
-  a.k = k;
-  a.mu = mu;
-  a.full = full;
-  a.nesterov = nesterov;
-  a.write_m = write_m;
-  a.elem = elem;
-  if (full) {
-    DIONW_REQUIRE(count > 0 && count <= kMaxTensors && blocks % count == 0,
-                  "prepare_ns_input: every-row mode takes 1..%d gradients dividing the blocks",
-                  kMaxTensors);
-    a.t.count = count;
-    for (int i = 0; i < count; ++i) {
-      DIONW_REQUIRE(grads[i], "prepare_ns_input: null gradient %d", i);
-      a.t.grad[i] = grads[i];
-    }
-    a.blocks_per_tensor = blocks / count;
-  } else {
-    a.blocks_per_tensor = blocks;
-  }
-  a.vec = (cols % 4 == 0) && (!momentum || aligned16(momentum)) &&
-          (!full || table_aligned(a.t, cols));
-  if (elem == kF32) {
-    DIONW_REQUIRE(out_transposed == nullptr, "prepare_ns_input: fp32 output has no transpose");
-    a.p_pad = k;
-    a.j_pad = cols;
-    dim3 grid((unsigned)std::min<int64_t>(ceil_div(cols, 256), 64), (unsigned)k,
-              (unsigned)blocks);
-    hipLaunchKernelGGL(prepare_raw_kernel, grid, dim3(256), 0, stream, a);
-    return check_launch("prepare_ns_input");
-  }
-  DIONW_REQUIRE(p_pad >= k && j_pad >= cols && p_pad % 8 == 0 && j_pad % 8 == 0,
-                "prepare_ns_input: padded extents must cover the block and be multiples of 8");
-  a.p_pad = p_pad;
-  a.j_pad = j_pad;
-  dim3 grid((unsigned)ceil_div(j_pad, kTile), (unsigned)ceil_div(p_pad, kTile), (unsigned)blocks);
-  DIONW_REQUIRE(blocks <= 65535 && grid.y <= 65535, "prepare_ns_input: grid too large");
-  if (elem == kF16)
-    hipLaunchKernelGGL(prepare_kernel<kF16>, grid, dim3(256), 0, stream, a);
+  if (elem != kF32)
+    DIONW_REQUIRE(p_pad >= k && j_pad >= cols && p_pad % 8 == 0 && j_pad % 8 == 0,
+                  "prepare_ns_input: padded extents must cover the block and be multiples of 8");
   else
-    hipLaunchKernelGGL(prepare_kernel<kBF16>, grid, dim3(256), 0, stream, a);
-  return check_launch("prepare_ns_input");
+    DIONW_REQUIRE(out_transposed == nullptr, "prepare_ns_input: fp32 output has no transpose");
+  if (blocks == 0) return kOk;
+  if (full) DIONW_REQUIRE(count > 0 && blocks % count == 0,
+                          "prepare_ns_input: every-row mode needs gradients dividing the blocks");
+  const int64_t bpt = full ? blocks / count : blocks;
+  const int64_t out_elems = elem == kF32 ? k * cols : p_pad * j_pad;  // per block
+  const size_t out_size = elem == kF32 ? 4 : 2;
+  // Every-row mode walks the gradient list kMaxTensors at a time; selected mode
+  // needs no table and runs in one launch.
+  const int32_t chunks = full ? (int32_t)ceil_div(count, kMaxTensors) : 1;
+  for (int32_t chunk = 0; chunk < chunks; ++chunk) {
+    PrepArgs a{};
+    int64_t b0 = 0, nb = blocks;
+    if (full) {
+      const int32_t t0 = chunk * kMaxTensors;
+      a.t.count = std::min<int32_t>(kMaxTensors, count - t0);
+      for (int i = 0; i < a.t.count; ++i) {
+        DIONW_REQUIRE(grads[t0 + i], "prepare_ns_input: null gradient %d", t0 + i);
+        a.t.grad[i] = grads[t0 + i];
+      }
+      b0 = (int64_t)t0 * bpt;
+      nb = (int64_t)a.t.count * bpt;
+    }
+    a.momentum = momentum ? momentum + b0 * rows * cols : nullptr;
+    a.idx = idx;
+    a.den = den + b0;
+    a.out_r = static_cast<char*>(out_rowmajor) + b0 * out_elems * out_size;
+    a.out_t = out_transposed ? static_cast<char*>(out_transposed) + b0 * out_elems * out_size
+                             : nullptr;
+    a.rows = rows;
+    a.cols = cols;
+    a.k = k;
+    a.mu = mu;
+    a.full = full;
+    a.nesterov = nesterov;
+    a.write_m = write_m;
+    a.elem = elem;
+    a.blocks_per_tensor = bpt;
+    a.vec = (cols % 4 == 0) && (!a.momentum || aligned16(a.momentum)) &&
+            (!full || table_aligned(a.t, cols));
+    if (elem == kF32) {
+      a.p_pad = k;
+      a.j_pad = cols;
+      dim3 grid((unsigned)std::min<int64_t>(ceil_div(cols, 256), 64), (unsigned)k, (unsigned)nb);
+      DIONW_REQUIRE(nb <= 65535 && k <= 65535, "prepare_ns_input: grid too large");
+      hipLaunchKernelGGL(prepare_raw_kernel, grid, dim3(256), 0, stream, a);
+    } else {
+      a.p_pad = p_pad;
+      a.j_pad = j_pad;
+      dim3 grid((unsigned)ceil_div(j_pad, kTile), (unsigned)ceil_div(p_pad, kTile), (unsigned)nb);
+      DIONW_REQUIRE(nb <= 65535 && grid.y <= 65535, "prepare_ns_input: grid too large");
+      if (elem == kF16)
+        hipLaunchKernelGGL(prepare_kernel<kF16>, grid, dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL(prepare_kernel<kBF16>, grid, dim3(256), 0, stream, a);
+    }
+    DIONW_TRY(check_launch("prepare_ns_input"));
+  }
+  return kOk;
 }
 
 }  // extern "C"

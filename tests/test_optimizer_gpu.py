@@ -269,6 +269,29 @@ def test_gpu_ema_schedule() -> None:
     torch.testing.assert_close(opt.state[p]["ema_shadow"], expected, rtol=1e-6, atol=0)
 
 
+@pytest.mark.parametrize("nesterov", [False, True])
+def test_every_row_run_with_more_tensors_than_one_table(nesterov: bool) -> None:
+    """A run of 60 same-shape parameters (more than one 48-entry pointer table)
+    on the every-row path: momentum bit-exact, updates as the oracle's."""
+    g = torch.Generator().manual_seed(11)
+    starts = torch.randn(60, 64, 96, generator=g) * 0.02
+    params = [nn.Parameter(s.clone().to(DEV)) for s in starts]
+    opt = _dion(params, 1.0, kind=NewtonSchulz.KELLER_TRITON, normuon=not nesterov,
+                nesterov=nesterov, weight_decay=0.05)
+    grads = torch.randn(60, 64, 96, generator=g) * 1e-3
+    for p, gr in zip(params, grads):
+        p.grad = gr.to(DEV)
+    opt.step()
+    w, mom, var = starts.clone(), torch.zeros_like(starts), torch.zeros(60, 64, 1)
+    dion_ref.step_blocks(w, grads, mom, var, k=64, lr=LR, mu=0.95, beta2=0.95, weight_decay=0.05,
+                         kind="keller_triton", normuon=not nesterov, nesterov=nesterov)
+    got_m = torch.stack([opt.state[p]["momentum"].cpu() for p in params])
+    assert torch.equal(got_m, mom)
+    decay = 1 - LR * 0.05
+    got = torch.stack([p.detach().cpu() for p in params])
+    assert rel_fro(got - starts * decay, w - starts * decay) < 3e-2
+
+
 def test_muon_update_matches_oracle() -> None:
     """MUON_UPDATE: Nesterov momentum, Keller quintic, no row normalization."""
     g = torch.Generator().manual_seed(8)
