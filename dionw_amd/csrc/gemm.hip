@@ -540,200 +540,6 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
       g, acc, bidx, m0, n0, wm * WTM, wn * WTN, g.sym && tm == tn, smem);
 }
 
-// ---- hand-scheduled 256x256 kernel -----------------------------------------------
-//
-// 4 waves of 128x128 (16 AGPR accumulators each, one wave per SIMD), BK = 32,
-// 4-stage LDS ring refilled 4 stages ahead. Fragment registers are double
-// buffered: while the 16 MFMAs of one 16-deep k step run, the 8 fragment reads
-// of the next step (and, in the second half, the 8 direct-to-LDS loads of a
-// future stage) are interleaved between them by sched_group_barrier. The one
-// barrier per stage sits between the two halves, after which the stage just
-// consumed is refilled; its reads have completed (lgkmcnt(0)) in every wave.
-
-constexpr int HBM_ = 256, HSTAGES = 4;
-constexpr int HSTAGE_ELEMS = 2 * HBM_ * PBK;
-constexpr int HLOADS = HBM_ * PBK / 8 / 256;  // 4 per operand per thread
-
-// Instruction order of one half step (16 MFMAs, 8 fragment reads).
-#ifndef DIONW_SCHED_ORDER
-#define DIONW_SCHED_ORDER 1
-#endif
-__device__ __forceinline__ void sched_half() {
-#if DIONW_SCHED_ORDER == 0
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
-  }
-#else
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the next step's 8 reads first
-  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-#endif
-}
-
-template <typename T, typename OUT_T, int MODE>
-__global__ __launch_bounds__(256, 1) void gemm_nt_sched_kernel(GemmArgs g, int batch) {
-  constexpr int WT = 128, F = 4;
-  using V = typename Mfma<T>::vec;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  T* lds = reinterpret_cast<T*>(smem);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const int tiles = g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
-  const int total = tiles * batch;
-  int w = blockIdx.x;
-  {
-    const int per = total / 8, extra = total % 8, x = w % 8, i = w / 8;
-    w = x * per + min(x, extra) + i;
-  }
-  const int64_t bidx = w / tiles;
-  const int t = w - (int)bidx * tiles;
-  int tm, tn;
-  if (g.sym) {
-    tri_tile(t, tm, tn);
-  } else {
-    const int group = 8 * g.tiles_n;
-    const int first = (t / group) * 8;
-    const int gm = min(g.tiles_m - first, 8);
-    tm = first + (t % group) % gm;
-    tn = (t % group) / gm;
-  }
-  const int m0 = tm * HBM_, n0 = tn * HBM_;
-  const T* A = reinterpret_cast<const T*>(g.a) + bidx * g.sa;
-  const T* B = reinterpret_cast<const T*>(g.b) + bidx * g.sb;
-  const T* a_src[HLOADS];
-  const T* b_src[HLOADS];
-#pragma unroll
-  for (int j = 0; j < HLOADS; ++j) {
-    const int pos = (wave * HLOADS + j) * 64 + lane;
-    const int row = pos >> 2, logical = (pos & 3) ^ ((row >> 2) & 3);
-    a_src[j] = A + (int64_t)min(m0 + row, g.m - 1) * g.lda + logical * 8;
-    b_src[j] = B + (int64_t)min(n0 + row, g.n - 1) * g.ldb + logical * 8;
-  }
-  auto issue = [&](int kt) {
-    T* stage = lds + (kt % HSTAGES) * HSTAGE_ELEMS;
-    const int k0 = kt * PBK;
-#pragma unroll
-    for (int j = 0; j < HLOADS; ++j) {
-      __builtin_amdgcn_global_load_lds((const void*)(a_src[j] + k0),
-                                       (lds_ptr_t)(stage + (wave * HLOADS + j) * 512), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(b_src[j] + k0),
-                                       (lds_ptr_t)(stage + HBM_ * PBK + (wave * HLOADS + j) * 512),
-                                       16, 0, 0);
-    }
-  };
-  const int lrow = lane & 31, lk = lane >> 5;
-  int a_off[F], b_off[F][2];
-#pragma unroll
-  for (int i = 0; i < F; ++i) {
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      b_off[i][ks] = HBM_ * PBK + plds_off(wn * WT + i * 32 + lrow, 2 * ks + lk);
-    }
-    a_off[i] = plds_off(wm * WT + i * 32 + lrow, lk);  // ks = 0; ks = 1 is chunk ^ 2
-  }
-  auto read = [&](V (&af)[F], V (&bf)[F], const T* stage, int ks) {
-#pragma unroll
-    for (int i = 0; i < F; ++i) {
-      const int off = ks ? plds_off(wm * WT + i * 32 + lrow, 2 + lk) : a_off[i];
-      af[i] = *reinterpret_cast<const V*>(stage + off);
-    }
-#pragma unroll
-    for (int j = 0; j < F; ++j) bf[j] = *reinterpret_cast<const V*>(stage + b_off[j][ks]);
-  };
-
-  f32x16 acc[F][F];
-#pragma unroll
-  for (int i = 0; i < F; ++i)
-#pragma unroll
-    for (int j = 0; j < F; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-  const int kt_count = g.k / PBK;
-  for (int s = 0; s < HSTAGES; ++s)
-    if (s < kt_count) issue(s);
-  // Stage 0 ready: allow the loads of stages 1..3 to stay in flight.
-  if (kt_count >= 4) wait_vm_lgkm0<6 * HLOADS>();
-  else if (kt_count == 3) wait_vm_lgkm0<4 * HLOADS>();
-  else if (kt_count == 2) wait_vm_lgkm0<2 * HLOADS>();
-  else wait_vm_lgkm0<0>();
-  __builtin_amdgcn_s_barrier();
-  V a_cur[F], b_cur[F], a_nxt[F], b_nxt[F];
-  read(a_cur, b_cur, lds, 0);
-
-  for (int kt = 0; kt < kt_count; ++kt) {
-    const T* stage = lds + (kt % HSTAGES) * HSTAGE_ELEMS;
-    // First half: MFMAs of (kt, k step 0), reads of (kt, k step 1).
-    read(a_nxt, b_nxt, stage, 1);
-#pragma unroll
-    for (int i = 0; i < F; ++i)
-#pragma unroll
-      for (int j = 0; j < F; ++j) acc[i][j] = Mfma<T>::run(a_cur[i], b_cur[j], acc[i][j]);
-    sched_half();
-    // Stage kt + 1 complete in every wave, stage kt fully read: meet, refill.
-    const int ahead = min(2, kt_count - 2 - kt);  // stages after kt + 1 still loading
-    if (ahead >= 2) wait_vm_lgkm0<4 * HLOADS>();
-    else if (ahead == 1) wait_vm_lgkm0<2 * HLOADS>();
-    else wait_vm_lgkm0<0>();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    const bool refill = kt + HSTAGES < kt_count;
-    if (refill) issue(kt + HSTAGES);
-    const T* next_stage = lds + ((kt + 1) % HSTAGES) * HSTAGE_ELEMS;
-    // Second half: MFMAs of (kt, k step 1), reads of (kt + 1, k step 0) (on the
-    // last stage these read a stale, in-bounds stage and are never used).
-    read(a_cur, b_cur, next_stage, 0);
-#pragma unroll
-    for (int i = 0; i < F; ++i)
-#pragma unroll
-      for (int j = 0; j < F; ++j) acc[i][j] = Mfma<T>::run(a_nxt[i], b_nxt[j], acc[i][j]);
-    sched_half();
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  staged_epilogue<T, OUT_T, MODE, 256, HBM_, HBM_, F, F>(g, acc, bidx, m0, n0, wm * WT, wn * WT,
-                                                        g.sym && tm == tn, smem);
-}
-
-template <typename T, typename OUT_T, int MODE>
-int launch_sched(const Problem& p, hipStream_t stream) {
-  GemmArgs g = p.g;
-  g.ct_vec = !g.ct || (g.ldct % 4 == 0 && g.sct % 4 == 0 &&
-                       (reinterpret_cast<uintptr_t>(g.ct) & 7) == 0);
-  if (g.c_diag && g.sym) g.ct_vec = g.ct_vec && g.ldc % 4 == 0 && g.sc % 4 == 0;
-  constexpr size_t pipe_bytes = (size_t)HSTAGES * HSTAGE_ELEMS * 2;
-  constexpr size_t lds_bytes = pipe_bytes > epi_lds_bytes<HBM_, HBM_>() ? pipe_bytes
-                                                                     : epi_lds_bytes<HBM_, HBM_>();
-  auto kern = gemm_nt_sched_kernel<T, OUT_T, MODE>;
-  static std::once_flag once;
-  static hipError_t attr_rc = hipSuccess;
-  std::call_once(once, [&] {
-    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-  });
-  if (attr_rc != hipSuccess) {
-    set_error("gemm: hipFuncSetAttribute failed: %s", hipGetErrorString(attr_rc));
-    return kHipError;
-  }
-  g.tiles_m = (g.m + HBM_ - 1) / HBM_;
-  g.tiles_n = (g.n + HBM_ - 1) / HBM_;
-  if (g.sym && g.m != g.n) {
-    set_error("gemm: symmetric mode needs a square output");
-    return kInvalid;
-  }
-  const int64_t tiles = g.sym ? (int64_t)g.tiles_m * (g.tiles_m + 1) / 2
-                              : (int64_t)g.tiles_m * g.tiles_n;
-  if (tiles * p.batch > INT32_MAX) {
-    set_error("gemm: grid too large");
-    return kInvalid;
-  }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * p.batch)), dim3(256), lds_bytes, stream, g,
-                     (int)p.batch);
-  return check_launch("gemm_nt_sched");
-}
-
 // ---- launch configuration ----------------------------------------------------
 
 
@@ -814,35 +620,32 @@ int launch_pipe(const Problem& p, hipStream_t stream) {
 
 template <typename T, typename OUT_T, int MODE>
 int launch_typed(const Problem& p, hipStream_t stream) {
-  // Large outputs: 128x128 tiles (4 waves of 64x64); small ones 64x64 tiles
-  // so that a batch of small blocks still fills the 256 CUs.
-  const int64_t big_tiles = p.batch * ((p.g.m + 127) / 128) * ((p.g.n + 127) / 128) /
-                            (p.g.sym ? 2 : 1);
-  const int64_t huge_tiles = p.batch * ((p.g.m + 255) / 256) * ((p.g.n + 255) / 256) /
-                             (p.g.sym ? 2 : 1);
-  if (p.g.k % PBK == 0 && huge_tiles >= 256) {
-// Tile configuration of the large products; 4 (256x256 tiles, 16 waves of
-// 64x64) measured fastest on the Llama-3-8B Newton-Schulz shapes.
-#ifndef DIONW_PIPE_CFG
-#define DIONW_PIPE_CFG 4
+  // Workgroups a tile size yields (symmetric products: upper-triangle tiles).
+  auto wgs = [&](int tile) {
+    const int64_t tm = (p.g.m + tile - 1) / tile, tn = (p.g.n + tile - 1) / tile;
+    return p.batch * (p.g.sym ? tm * (tm + 1) / 2 : tm * tn);
+  };
+  const bool pipe_ok = p.g.k % PBK == 0;
+  using Big = PipeCfg<256, 256, 4, 4, 4>;  // 256x256 tiles, 16 waves of 64x64
+  using Mid = PipeCfg<128, 128, 2, 2, 4>;  // 128x128 tiles, 4 waves of 64x64
+#ifdef DIONW_FORCE_KERNEL
+  // Tuning builds only: one kernel for every product it can run.
+  if (DIONW_FORCE_KERNEL == 1 && pipe_ok) return launch_pipe<T, OUT_T, MODE, Big>(p, stream);
+  if (DIONW_FORCE_KERNEL == 2 && pipe_ok) return launch_pipe<T, OUT_T, MODE, Mid>(p, stream);
+  if (DIONW_FORCE_KERNEL == 3) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
+  if (DIONW_FORCE_KERNEL == 4) return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
 #endif
-#if DIONW_PIPE_CFG == 0
-    return launch_pipe<T, OUT_T, MODE, PipeCfg<256, 256, 2, 4, 4>>(p, stream);
-#elif DIONW_PIPE_CFG == 1
-    return launch_pipe<T, OUT_T, MODE, PipeCfg<256, 256, 2, 4, 3>>(p, stream);
-#elif DIONW_PIPE_CFG == 2
-    return launch_pipe<T, OUT_T, MODE, PipeCfg<128, 128, 2, 2, 4>>(p, stream);
-#elif DIONW_PIPE_CFG == 3
-    return launch_pipe<T, OUT_T, MODE, PipeCfg<128, 128, 2, 2, 3>>(p, stream);
-#elif DIONW_PIPE_CFG == 4
-    return launch_pipe<T, OUT_T, MODE, PipeCfg<256, 256, 4, 4, 4>>(p, stream);
-#elif DIONW_PIPE_CFG == 5
-    return launch_pipe<T, OUT_T, MODE, PipeCfg<128, 128, 2, 2, 2>>(p, stream);
-#elif DIONW_PIPE_CFG == 6
-    return launch_sched<T, OUT_T, MODE>(p, stream);
-#endif
+  if (pipe_ok) {
+    // Rounds of workgroups over the 256 CUs (one 256x256 or two 128x128 per CU)
+    // times the tile's work over the tile's measured efficiency (0.85 and 0.70 of
+    // the CU's MFMA rate on the large shapes): the smaller tile wins when the big
+    // one leaves CUs idle or pads a ragged side.
+    const double big = (double)((wgs(256) + 255) / 256) * (256.0 * 256.0) / 0.85;
+    const double mid = (double)((wgs(128) + 511) / 512) * (2.0 * 128.0 * 128.0) / 0.70;
+    if (big <= mid) return launch_pipe<T, OUT_T, MODE, Big>(p, stream);
+    return launch_pipe<T, OUT_T, MODE, Mid>(p, stream);
   }
-  if (big_tiles >= 512) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
+  if (wgs(128) >= 512) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
   return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
 }
 
