@@ -2,7 +2,8 @@
 //
 // Every product is one "NT" form, C[i,j] = sum_k A[i,k] B[j,k] with both
 // operands row-major along k, computed with v_mfma_f32_32x32x16_{f16,bf16}
-// (fp32 accumulation) from LDS-staged 64-deep k tiles. The epilogue forms
+// (fp32 accumulation) from LDS-staged k tiles (64 deep; 32 deep where k is an
+// odd multiple of 32). The epilogue forms
 // alpha * acc + beta * D[i,j] and rounds once to the storage type.
 //
 //  symmetric mode  only tiles on and above the diagonal are computed and each
@@ -281,26 +282,32 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmArgs g) {
 // same number of loads per stage and the vmcnt arithmetic is exact; k must be
 // a multiple of 32.
 
-constexpr int PBK = 32;  // k depth of one LDS stage
-
-// Tile configuration: BM x BN output tile, WM x WN waves, STAGES-deep LDS ring.
-template <int BM_, int BN_, int WM_, int WN_, int STAGES_>
+// Tile configuration: BM x BN output tile, WM x WN waves, STAGES-deep LDS ring of
+// BK-deep stages.
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int BK_>
 struct PipeCfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_, BK = BK_;
   static constexpr int threads = WM * WN * 64;
-  static constexpr int stage_elems = (BM + BN) * PBK;         // A then B
-  static constexpr int loads_a = BM * PBK / 8 / threads;      // 16-byte loads per thread
-  static constexpr int loads_b = BN * PBK / 8 / threads;
+  static constexpr int stage_elems = (BM + BN) * BK;          // A then B
+  static constexpr int loads_a = BM * BK / 8 / threads;       // 16-byte loads per thread
+  static constexpr int loads_b = BN * BK / 8 / threads;
   static constexpr size_t lds_bytes = (size_t)STAGES * stage_elems * 2;
   static_assert(loads_a >= 1 && loads_b >= 1, "tile too small for the thread count");
+  static_assert(BK == 32 || BK == 64, "stage depth 32 or 64");
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Chunk q (16 bytes, 0..3) of row r sits at q ^ ((r >> 2) & 3): the 16 lanes
-// of a read phase (rows r..r+15, same chunk) cover all 64 banks once.
+// A stage row holds BK/8 chunks of 16 bytes. Chunk q of row r sits at
+// q ^ ((r >> 2) & 3) (BK 32) or q ^ ((r >> 1) & 7) (BK 64): the 16 lanes of a
+// read phase (rows r..r+15, same chunk) cover all 64 banks once.
+template <int BK>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return BK == 32 ? chunk ^ ((row >> 2) & 3) : chunk ^ ((row >> 1) & 7);
+}
+template <int BK>
 __device__ __forceinline__ int plds_off(int row, int chunk) {
-  return row * PBK + ((chunk ^ ((row >> 2) & 3)) << 3);
+  return row * BK + (swz<BK>(row, chunk) << 3);
 }
 
 // ---- LDS-staged epilogue of the large-tile kernels ------------------------------
@@ -433,6 +440,7 @@ template <typename T, typename OUT_T, int MODE, typename CFG>
 __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs g, int batch) {
   constexpr int PBM = CFG::BM, PBN = CFG::BN, PWN = CFG::WN, PSTAGES = CFG::STAGES;
   constexpr int PSTAGE_ELEMS = CFG::stage_elems, LA = CFG::loads_a, LB = CFG::loads_b;
+  constexpr int SBK = CFG::BK, CPR = SBK / 8;  // stage depth, 16-byte chunks per row
   constexpr int WTM = PBM / CFG::WM, WTN = PBN / PWN;  // wave tile
   constexpr int FM = WTM / 32, FN = WTN / 32;      // 32x32 fragments
   using V = typename Mfma<T>::vec;
@@ -474,18 +482,18 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
 #pragma unroll
   for (int j = 0; j < LA; ++j) {
     const int pos = (wave * LA + j) * 64 + lane;  // 16-byte chunk index
-    const int row = pos >> 2, logical = (pos & 3) ^ ((row >> 2) & 3);
+    const int row = pos / CPR, logical = swz<SBK>(row, pos % CPR);
     a_src[j] = A + (int64_t)min(m0 + row, g.m - 1) * g.lda + logical * 8;
   }
 #pragma unroll
   for (int j = 0; j < LB; ++j) {
     const int pos = (wave * LB + j) * 64 + lane;
-    const int row = pos >> 2, logical = (pos & 3) ^ ((row >> 2) & 3);
+    const int row = pos / CPR, logical = swz<SBK>(row, pos % CPR);
     b_src[j] = B + (int64_t)min(n0 + row, g.n - 1) * g.ldb + logical * 8;
   }
   auto issue = [&](int kt) {
     T* stage = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
-    const int k0 = kt * PBK;
+    const int k0 = kt * SBK;
 #pragma unroll
     for (int j = 0; j < LA; ++j)  // wave-uniform LDS destination: lane i lands at +16 i bytes
       __builtin_amdgcn_global_load_lds((const void*)(a_src[j] + k0),
@@ -493,7 +501,7 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
 #pragma unroll
     for (int j = 0; j < LB; ++j)
       __builtin_amdgcn_global_load_lds((const void*)(b_src[j] + k0),
-                                       (lds_ptr_t)(stage + PBM * PBK + (wave * LB + j) * 512), 16,
+                                       (lds_ptr_t)(stage + PBM * SBK + (wave * LB + j) * 512), 16,
                                        0, 0);
   };
 
@@ -505,7 +513,7 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int kt_count = g.k / PBK;
+  const int kt_count = g.k / SBK;
 #pragma unroll
   for (int s = 0; s < PSTAGES - 1; ++s)
     if (s < kt_count) issue(s);
@@ -519,16 +527,16 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
     __builtin_amdgcn_s_barrier();
     if (kt + PSTAGES - 1 < kt_count) issue(kt + PSTAGES - 1);
     const T* As = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
-    const T* Bs = As + PBM * PBK;
+    const T* Bs = As + PBM * SBK;
 #pragma unroll
-    for (int ks = 0; ks < PBK / 16; ++ks) {
+    for (int ks = 0; ks < SBK / 16; ++ks) {
       V af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const V*>(As + plds_off(wm * WTM + i * 32 + lrow, 2 * ks + lk));
+        af[i] = *reinterpret_cast<const V*>(As + plds_off<SBK>(wm * WTM + i * 32 + lrow, 2 * ks + lk));
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const V*>(Bs + plds_off(wn * WTN + j * 32 + lrow, 2 * ks + lk));
+        bfr[j] = *reinterpret_cast<const V*>(Bs + plds_off<SBK>(wn * WTN + j * 32 + lrow, 2 * ks + lk));
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -625,25 +633,41 @@ int launch_typed(const Problem& p, hipStream_t stream) {
     const int64_t tm = (p.g.m + tile - 1) / tile, tn = (p.g.n + tile - 1) / tile;
     return p.batch * (p.g.sym ? tm * (tm + 1) / 2 : tm * tn);
   };
-  const bool pipe_ok = p.g.k % PBK == 0;
-  using Big = PipeCfg<256, 256, 4, 4, 4>;  // 256x256 tiles, 16 waves of 64x64
-  using Mid = PipeCfg<128, 128, 2, 2, 4>;  // 128x128 tiles, 4 waves of 64x64
+  // 256x256 tiles run 16 waves of 64x64, 128x128 tiles 4 waves of 64x64. A k
+  // depth that is a multiple of 64 takes 64-deep stages in a two-stage ring (half
+  // the barriers per MFMA of 32-deep stages); other multiples of 32, four
+  // 32-deep stages.
+  using Big64 = PipeCfg<256, 256, 4, 4, 2, 64>;
+  using Mid64 = PipeCfg<128, 128, 2, 2, 2, 64>;
+  using Big32 = PipeCfg<256, 256, 4, 4, 4, 32>;
+  using Mid32 = PipeCfg<128, 128, 2, 2, 4, 32>;
+  const bool k64 = p.g.k % 64 == 0, k32 = p.g.k % 32 == 0;
 #ifdef DIONW_FORCE_KERNEL
-  // Tuning builds only: one kernel for every product it can run.
-  if (DIONW_FORCE_KERNEL == 1 && pipe_ok) return launch_pipe<T, OUT_T, MODE, Big>(p, stream);
-  if (DIONW_FORCE_KERNEL == 2 && pipe_ok) return launch_pipe<T, OUT_T, MODE, Mid>(p, stream);
+  // Tuning builds only: one tile shape for every product it can run.
+  if (DIONW_FORCE_KERNEL == 1 && k32) {
+    if (k64) return launch_pipe<T, OUT_T, MODE, Big64>(p, stream);
+    return launch_pipe<T, OUT_T, MODE, Big32>(p, stream);
+  }
+  if (DIONW_FORCE_KERNEL == 2 && k32) {
+    if (k64) return launch_pipe<T, OUT_T, MODE, Mid64>(p, stream);
+    return launch_pipe<T, OUT_T, MODE, Mid32>(p, stream);
+  }
   if (DIONW_FORCE_KERNEL == 3) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
   if (DIONW_FORCE_KERNEL == 4) return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
 #endif
-  if (pipe_ok) {
+  if (k32) {
     // Rounds of workgroups over the 256 CUs (one 256x256 or two 128x128 per CU)
-    // times the tile's work over the tile's measured efficiency (0.85 and 0.70 of
-    // the CU's MFMA rate on the large shapes): the smaller tile wins when the big
-    // one leaves CUs idle or pads a ragged side.
-    const double big = (double)((wgs(256) + 255) / 256) * (256.0 * 256.0) / 0.85;
-    const double mid = (double)((wgs(128) + 511) / 512) * (2.0 * 128.0 * 128.0) / 0.70;
-    if (big <= mid) return launch_pipe<T, OUT_T, MODE, Big>(p, stream);
-    return launch_pipe<T, OUT_T, MODE, Mid>(p, stream);
+    // times the work of one round, the 128x128 rounds weighted 1.2 (its measured
+    // rate on the large shapes is 1/1.2 of the 256x256 tile's): the smaller tile
+    // wins when the big one leaves CUs idle or pads a ragged side.
+    const double big = (double)((wgs(256) + 255) / 256) * (256.0 * 256.0);
+    const double mid = (double)((wgs(128) + 511) / 512) * (2.0 * 128.0 * 128.0) * 1.2;
+    if (big <= mid) {
+      if (k64) return launch_pipe<T, OUT_T, MODE, Big64>(p, stream);
+      return launch_pipe<T, OUT_T, MODE, Big32>(p, stream);
+    }
+    if (k64) return launch_pipe<T, OUT_T, MODE, Mid64>(p, stream);
+    return launch_pipe<T, OUT_T, MODE, Mid32>(p, stream);
   }
   if (wgs(128) >= 512) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
   return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);

@@ -99,8 +99,12 @@ def test_accumulate_copy_decay(nesterov: bool) -> None:
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize(("batch", "m", "n", "k"), [(1, 64, 64, 64), (3, 100, 72, 136),
                                                     (2, 256, 512, 1024), (5, 352, 352, 2048),
-                                                    # large enough for the pipelined 256x256 kernel
-                                                    (20, 1024, 1024, 512), (20, 1000, 1032, 512)])
+                                                    # pipelined 128x128 tiles, 64-deep stages
+                                                    (20, 1024, 1024, 512), (20, 1000, 1032, 512),
+                                                    # pipelined 128x128 tiles, 32-deep stages
+                                                    (20, 1024, 1024, 352),
+                                                    # pipelined 256x256 tiles, 64- and 32-deep
+                                                    (64, 1024, 1024, 512), (64, 1000, 1032, 352)])
 def test_gemm_nt_matches_fp32(dtype: torch.dtype, batch: int, m: int, n: int, k: int) -> None:
     g = _gen(3)
     a = torch.randn(batch, m, k, generator=g).to(dtype)
