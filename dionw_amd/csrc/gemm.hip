@@ -521,6 +521,7 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
   for (int kt = 0; kt < kt_count; ++kt) {
     const int ahead = min(PSTAGES - 2, kt_count - 1 - kt);  // stages issued after kt
     static_assert(PSTAGES >= 2 && PSTAGES <= 4, "waits cover 0..2 stages ahead");
+    static_assert(2 * (LA + LB) <= 63, "vmcnt counts to 63");
     if (ahead >= 2) wait_vm_lgkm0<2 * (LA + LB)>();
     else if (ahead == 1) wait_vm_lgkm0<LA + LB>();
     else wait_vm_lgkm0<0>();
@@ -528,19 +529,28 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
     if (kt + PSTAGES - 1 < kt_count) issue(kt + PSTAGES - 1);
     const T* As = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
     const T* Bs = As + PBM * SBK;
-#pragma unroll
-    for (int ks = 0; ks < SBK / 16; ++ks) {
-      V af[FM], bfr[FN];
+    // Fragments of k-step ks + 1 are read while the MFMAs of k-step ks run.
+    V af[2][FM], bfr[2][FN];
+    auto frag = [&](int ks, int set) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const V*>(As + plds_off<SBK>(wm * WTM + i * 32 + lrow, 2 * ks + lk));
+        af[set][i] = *reinterpret_cast<const V*>(As + plds_off<SBK>(wm * WTM + i * 32 + lrow, 2 * ks + lk));
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const V*>(Bs + plds_off<SBK>(wn * WTN + j * 32 + lrow, 2 * ks + lk));
+        bfr[set][j] = *reinterpret_cast<const V*>(Bs + plds_off<SBK>(wn * WTN + j * 32 + lrow, 2 * ks + lk));
+    };
+    frag(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < SBK / 16; ++ks) {
+      if (ks + 1 < SBK / 16) frag(ks + 1, (ks + 1) & 1);
+      // Without this fence the scheduler sinks the reads below the MFMAs and the
+      // two fragment sets share registers again.
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<T>::run(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = Mfma<T>::run(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
     }
   }
 
