@@ -45,12 +45,18 @@ struct AdamScalars {
 __device__ __forceinline__ void adamw_element(float& param_io, float grad, float& exp_avg_io,
                                               float& exp_avg_sq_io, const AdamScalars& s,
                                               float bias_correction1, float bias_correction2_sqrt) {
+  // The fused multiply-adds are spelled out (and contraction is off) so that
+  // the rounding does not depend on how the compiler schedules the caller's
+  // loop: this is the form that reproduces torch's fused AdamW bit for bit.
+#pragma clang fp contract(off)
   float param = param_io;
   float exp_avg = exp_avg_io;
   float exp_avg_sq = exp_avg_sq_io;
-  if (s.weight_decay != 0) param -= s.lr * s.weight_decay * param;
-  exp_avg = s.beta1 * exp_avg + (1 - s.beta1) * grad;
-  exp_avg_sq = s.beta2 * exp_avg_sq + (1 - s.beta2) * grad * grad;
+  const double g = grad;
+  if (s.weight_decay != 0)
+    param = (float)__builtin_fma(-(s.lr * s.weight_decay), (double)param, (double)param);
+  exp_avg = (float)__builtin_fma(s.beta1, (double)exp_avg, (1 - s.beta1) * g);
+  exp_avg_sq = (float)__builtin_fma(s.beta2, (double)exp_avg_sq, ((1 - s.beta2) * g) * g);
   const float step_size = s.lr / bias_correction1;
   const float denom = (std::sqrt(exp_avg_sq) / bias_correction2_sqrt) + s.eps;
   param -= step_size * exp_avg / denom;
@@ -75,11 +81,11 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s) 
                      reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
   int64_t i = 0;
   if (vec) {
-    for (int64_t q = threadIdx.x; 4 * q + 3 < end; q += 256) {
-      f32x4 pv = reinterpret_cast<f32x4*>(p)[q];
-      const f32x4 gv = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g) + q);
-      f32x4 mv = reinterpret_cast<f32x4*>(m)[q];
-      f32x4 vv = reinterpret_cast<f32x4*>(v)[q];
+    f32x4* p4 = reinterpret_cast<f32x4*>(p);
+    const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
+    f32x4* m4 = reinterpret_cast<f32x4*>(m);
+    f32x4* v4 = reinterpret_cast<f32x4*>(v);
+    auto update = [&](int64_t q, f32x4 pv, f32x4 gv, f32x4 mv, f32x4 vv) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float pe = pv[e], me = mv[e], ve = vv[e];
@@ -88,10 +94,22 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s) 
         mv[e] = me;
         vv[e] = ve;
       }
-      reinterpret_cast<f32x4*>(p)[q] = pv;
-      reinterpret_cast<f32x4*>(m)[q] = mv;
-      reinterpret_cast<f32x4*>(v)[q] = vv;
+      p4[q] = pv;
+      m4[q] = mv;
+      v4[q] = vv;
+    };
+    const int64_t n4 = end >> 2;
+    int64_t q = threadIdx.x;
+    // Two chunks per iteration: eight 16-byte loads in flight per lane.
+    for (; q + 256 < n4; q += 512) {
+      const f32x4 pa = p4[q], pb = p4[q + 256];
+      const f32x4 ga = __builtin_nontemporal_load(g4 + q);
+      const f32x4 gb = __builtin_nontemporal_load(g4 + q + 256);
+      const f32x4 ma = m4[q], mb = m4[q + 256], va = v4[q], vb = v4[q + 256];
+      update(q, pa, ga, ma, va);
+      update(q + 256, pb, gb, mb, vb);
     }
+    for (; q < n4; q += 256) update(q, p4[q], __builtin_nontemporal_load(g4 + q), m4[q], v4[q]);
     i = end & ~(int64_t)3;
   }
   for (int64_t e = i + threadIdx.x; e < end; e += 256) {

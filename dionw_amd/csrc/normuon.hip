@@ -105,18 +105,19 @@ __device__ __forceinline__ float update_one(float w, float o, float d, float s,
   return w + n * s;
 }
 
-__global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// One 256-thread workgroup per row (a row sweep of 4 KiB per step streams
+// faster than a wavefront per row).
+constexpr int kApplyThreads = 256;
+
+__global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
+  const int tid = threadIdx.x;
+  const int64_t r = blockIdx.x;  // the grid has exactly one workgroup per row
   int64_t gr, slot, b;
   if (a.only_selected) {
-    const int64_t total = (int64_t)a.t.count * (a.rows_per_tensor / a.rows) * a.k;
-    if (r >= total) return;
     b = r / a.k;
     slot = r - b * a.k;
     gr = b * a.rows + a.idx[r];
   } else {
-    if (r >= (int64_t)a.t.count * a.rows_per_tensor) return;
     gr = r;
     b = gr / a.rows;
     const int64_t in_block = gr - b * a.rows;
@@ -125,13 +126,24 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
   const int tensor = (int)(gr / a.rows_per_tensor);
   float* w = a.t.param[tensor] + (gr - (int64_t)tensor * a.rows_per_tensor) * a.cols;
   const bool apply_decay = a.apply_decay != 0;
+  constexpr int U = 4;  // chunks whose loads are issued together
+  constexpr int T = kApplyThreads;
   if (slot < 0) {
     if (!apply_decay) return;
     if (a.vec) {
       f32x4* w4 = reinterpret_cast<f32x4*>(w);
-      for (int64_t c = lane; c < (a.cols >> 2); c += kWave) w4[c] = w4[c] * a.decay;
+      const int64_t n4 = a.cols >> 2;
+      int64_t c = tid;
+      for (; c + (U - 1) * T < n4; c += U * T) {
+        f32x4 wv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) wv[u] = w4[c + u * T];
+#pragma unroll
+        for (int u = 0; u < U; ++u) w4[c + u * T] = wv[u] * a.decay;
+      }
+      for (; c < n4; c += T) w4[c] = w4[c] * a.decay;
     } else {
-      for (int64_t c = lane; c < a.cols; c += kWave) w[c] = w[c] * a.decay;
+      for (int64_t c = tid; c < a.cols; c += T) w[c] = w[c] * a.decay;
     }
     return;
   }
@@ -143,16 +155,28 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
   if (a.vec) {
     f32x4* w4 = reinterpret_cast<f32x4*>(w);
     const bf16x4* o4 = reinterpret_cast<const bf16x4*>(o);
-    for (int64_t c = lane; c < (a.cols >> 2); c += kWave) {
-      f32x4 wv = w4[c];
-      bf16x4 ov = o4[c];
+    auto upd = [&](f32x4 wv, bf16x4 ov) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         wv[e] = update_one(wv[e], (float)ov[e], d, s, normalized, a.decay, apply_decay);
-      w4[c] = wv;
+      return wv;
+    };
+    const int64_t n4 = a.cols >> 2;
+    int64_t c = tid;
+    for (; c + (U - 1) * T < n4; c += U * T) {
+      f32x4 wv[U];
+      bf16x4 ov[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        wv[u] = w4[c + u * T];
+        ov[u] = o4[c + u * T];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) w4[c + u * T] = upd(wv[u], ov[u]);
     }
+    for (; c < n4; c += T) w4[c] = upd(w4[c], o4[c]);
   } else {
-    for (int64_t c = lane; c < a.cols; c += kWave)
+    for (int64_t c = tid; c < a.cols; c += T)
       w[c] = update_one(w[c], (float)o[c], d, s, normalized, a.decay, apply_decay);
   }
 }
@@ -228,7 +252,10 @@ int dionw_apply_update(float* const* params, int32_t count, int64_t blocks_per_t
     a.only_selected = !apply_decay && k < rows;
     const int64_t n = a.only_selected ? (int64_t)a.t.count * blocks_per_tensor * k
                                       : (int64_t)a.t.count * a.rows_per_tensor;
-    hipLaunchKernelGGL(apply_kernel, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, stream, a);
+    if (n == 0) continue;
+    DIONW_REQUIRE(n * kApplyThreads <= (int64_t)UINT32_MAX,
+                  "apply_update: %lld rows exceed one launch", (long long)n);
+    hipLaunchKernelGGL(apply_kernel, dim3((unsigned)n), dim3(kApplyThreads), 0, stream, a);
     DIONW_TRY(check_launch("apply_update"));
   }
   return kOk;

@@ -52,39 +52,43 @@ NORMALIZATION_EPS: Final = 1e-8        # _row_normalization.py:15
 def row_l1_scores(m: np.ndarray) -> np.ndarray:
     """Row l1 norms of float32 ``m`` [rows, cols] in the kernel's fixed order.
 
-    Follows the reduction of _momentum_kernels.py:44-55 (per-lane partial sums
-    over column chunks, then a tree) in the order the HIP kernel fixes: a lane
-    of 64 sums its float4 chunks ``lane, lane + 64, ...`` component-wise in
-    column order, combines ``(x + y) + (z + w)``, then lanes combine pairwise
-    (i, i + 32), (i, i + 16), ..., (i, i + 1). For cols % 4 != 0 the lane sums
-    the single elements ``lane, lane + 64, ...``.
+    Follows the reduction of _momentum_kernels.py:44-55 (per-thread partial
+    sums over column chunks, then a tree) in the order the HIP kernel fixes:
+    thread t of 256 sums its float4 chunks ``t, t + 256, ...`` component-wise in
+    column order and combines ``(x + y) + (z + w)``; within each of the four
+    waves (threads 64w .. 64w + 63) lanes combine pairwise (i, i + 32),
+    (i, i + 16), ..., (i, i + 1); the wave sums combine as (w0 + w1) + (w2 + w3).
+    For cols % 4 != 0 thread t sums the single elements ``t, t + 256, ...``.
     """
     m = np.ascontiguousarray(m, dtype=np.float32)
     rows, cols = m.shape
     a = np.abs(m)
+    threads = 256
     if cols % 4 == 0:
         n4 = cols // 4
-        steps = -(-n4 // 64)
-        padded = np.zeros((rows, steps * 64 * 4), np.float32)
+        steps = -(-n4 // threads)
+        padded = np.zeros((rows, steps * threads * 4), np.float32)
         padded[:, :cols] = a
-        chunks = padded.reshape(rows, steps, 64, 4)
-        part = np.zeros((rows, 64, 4), np.float32)
+        chunks = padded.reshape(rows, steps, threads, 4)
+        part = np.zeros((rows, threads, 4), np.float32)
         for j in range(steps):
             part = part + chunks[:, j]
         lanes = (part[..., 0] + part[..., 1]) + (part[..., 2] + part[..., 3])
     else:
-        steps = -(-cols // 64)
-        padded = np.zeros((rows, steps * 64), np.float32)
+        steps = -(-cols // threads)
+        padded = np.zeros((rows, steps * threads), np.float32)
         padded[:, :cols] = a
-        chunks = padded.reshape(rows, steps, 64)
-        lanes = np.zeros((rows, 64), np.float32)
+        chunks = padded.reshape(rows, steps, threads)
+        lanes = np.zeros((rows, threads), np.float32)
         for j in range(steps):
             lanes = lanes + chunks[:, j]
+    lanes = lanes.reshape(rows, 4, 64)
     off = 32
     while off >= 1:
-        lanes = lanes[:, :off] + lanes[:, off : 2 * off]
+        lanes = lanes[..., :off] + lanes[..., off : 2 * off]
         off //= 2
-    return lanes[:, 0].copy()
+    w = lanes[..., 0]
+    return ((w[:, 0] + w[:, 1]) + (w[:, 2] + w[:, 3])).astype(np.float32)
 
 
 def topk_rows(scores: np.ndarray, k: int) -> np.ndarray:
