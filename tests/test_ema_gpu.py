@@ -1,0 +1,246 @@
+"""The optimizer-integrated EMA on the GPU: schedule, GPU and CPU shadows,
+checkpoints, weight swaps (behaviour of tests/test_ema.py:89-520 of the
+reference, restated here).
+
+Shadows are checked against a plain torch lerp of the live weights; where the
+reference's tests demand exactness (swaps, checkpoints, a constant parameter)
+the checks here are exact too.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+from torch import nn
+
+import dionw_amd as dionw
+from dionw_amd import EMAConfig, EMADevice
+from dionw_amd.ema import no_profile
+
+pytestmark = pytest.mark.gpu
+
+
+def _config(device: EMADevice, decay: float, *, every: int = 1, start: int = 0,
+            final: float | None = None, ramp: int | None = None,
+            gamma: float | None = None) -> EMAConfig:
+    return EMAConfig(decay=decay, device=device, pin_memory=True, update_every_n_steps=every,
+                     start_step=start, decay_final=final, decay_ramp_steps=ramp,
+                     power_gamma=gamma)
+
+
+def _weights(seed: int = 0) -> tuple[nn.Parameter, nn.Parameter]:
+    """A 32 x 48 matrix (Dion route) and a 48-vector (AdamW route)."""
+    g = torch.Generator().manual_seed(seed)
+    return (nn.Parameter(torch.randn(32, 48, generator=g).cuda()),
+            nn.Parameter(torch.randn(48, generator=g).cuda()))
+
+
+def _dion(weights: tuple[nn.Parameter, nn.Parameter], ema: EMAConfig | None) -> dionw.Dion:
+    matrix, vector = weights
+    return dionw.Dion(
+        [{"params": [vector], dionw.ROUTE_KEY: "adamw"},
+         {"params": [matrix], dionw.ROUTE_KEY: "matrix", dionw.FRACTION_KEY: 0.5}],
+        lr=1e-2, momentum=0.95, muon_beta2=0.95, betas=(0.9, 0.99), weight_decay=0.0,
+        eps=1e-8, ema=ema)
+
+
+def _train(weights, opt, steps: int = 1, seed: int = 100) -> None:
+    g = torch.Generator().manual_seed(seed)
+    for _ in range(steps):
+        for w in weights:
+            w.grad = torch.randn(w.shape, generator=g).cuda()
+        opt.step()
+
+
+def _shadow(opt, w) -> torch.Tensor:
+    return opt.state[w]["ema_shadow"]
+
+
+@pytest.mark.parametrize("device", list(EMADevice))
+@pytest.mark.parametrize(("every", "start"), [(1, 0), (2, 0), (1, 3), (2, 3)])
+def test_shadow_tracks_a_lerp_of_the_live_weights(device: EMADevice, every: int,
+                                                  start: int) -> None:
+    decay = 0.8
+    weights = _weights()
+    opt = _dion(weights, _config(device, decay, every=every, start=start))
+    expected = None
+    for step in range(1, 10):
+        _train(weights, opt, seed=step)
+        live = [w.detach().clone() for w in weights]
+        if start:
+            if step < start or (step - start) % every:
+                continue
+            first = step == start
+        else:
+            if step % every:
+                continue
+            first = expected is None
+        expected = live if first else [e.lerp(x, 1 - decay**every)
+                                       for e, x in zip(expected, live)]
+    opt.ema.flush_pending_updates()
+    for w, e in zip(weights, expected):
+        s = _shadow(opt, w)
+        assert s.device.type == ("cuda" if device is EMADevice.GPU else "cpu")
+        torch.testing.assert_close(s.cuda(), e, rtol=1e-6, atol=1e-6)
+
+
+def test_swapped_flag_follows_swap_and_restore() -> None:
+    weights = _weights()
+    opt = _dion(weights, _config(EMADevice.GPU, 0.9))
+    assert not opt.ema_weights_swapped
+    _train(weights, opt)
+    assert opt.swap_ema_weights() and opt.ema_weights_swapped
+    assert opt.restore_non_ema_weights() and not opt.ema_weights_swapped
+
+
+@pytest.mark.parametrize("device", list(EMADevice))
+def test_checkpoint_restores_shadows_and_step_count(device: EMADevice) -> None:
+    weights = _weights()
+    config = _config(device, 0.9)
+    opt = _dion(weights, config)
+    _train(weights, opt, steps=3)
+    saved = opt.state_dict()
+    again = _dion(weights, config)
+    again.load_state_dict(saved)
+    assert again.ema.step_count == 3
+    for w in weights:
+        assert _shadow(again, w).device == _shadow(opt, w).device
+        assert torch.equal(_shadow(again, w), _shadow(opt, w))
+    with pytest.raises(ValueError, match="without EMA"):
+        _dion(weights, None).load_state_dict(saved)
+    with pytest.raises(ValueError, match="non-negative"):
+        again.ema.step_count = -1
+
+
+@pytest.mark.parametrize("device", list(EMADevice))
+def test_swap_puts_shadows_in_and_restore_takes_them_out(device: EMADevice) -> None:
+    weights = _weights()
+    opt = _dion(weights, _config(device, 0.5))
+    assert not opt.swap_ema_weights()  # nothing to swap before the first update
+    _train(weights, opt, steps=3)
+    live = [w.detach().clone() for w in weights]
+    assert opt.swap_ema_weights()
+    for w in weights:
+        assert torch.equal(w.detach(), _shadow(opt, w).cuda())
+    assert opt.restore_non_ema_weights()
+    for w, x in zip(weights, live):
+        assert torch.equal(w.detach(), x)
+
+
+def test_unchanging_parameter_keeps_an_exact_shadow() -> None:
+    weights = _weights()
+    opt = _dion(weights, _config(EMADevice.GPU, 0.999))
+    for group in opt.param_groups:
+        group["lr"] = 0.0
+    _train(weights, opt, steps=20)
+    for w in weights:
+        assert torch.equal(_shadow(opt, w), w.detach())
+
+
+def test_swap_guards_and_weights_without_gradients() -> None:
+    matrix, vector = weights = _weights()
+    opt = _dion(weights, _config(EMADevice.GPU, 0.5))
+    g = torch.Generator().manual_seed(7)
+    for _ in range(2):
+        matrix.grad = torch.randn(matrix.shape, generator=g).cuda()
+        opt.step()
+    # The vector never had a gradient: its shadow is still its value.
+    assert torch.equal(_shadow(opt, vector), vector.detach())
+    assert opt.swap_ema_weights()
+    with pytest.raises(RuntimeError, match="already swapped"):
+        opt.swap_ema_weights()
+    with pytest.raises(RuntimeError, match="swapped in"):
+        opt.step()
+    opt.restore_non_ema_weights()
+    opt.step()
+
+
+def test_swap_scoped_to_a_module() -> None:
+    weights = _weights()
+    opt = _dion(weights, _config(EMADevice.GPU, 0.5))
+    _train(weights, opt)
+    frozen = nn.Sequential(nn.Linear(4, 4).cuda().requires_grad_(False))
+    with pytest.raises(ValueError, match="no optimizer-managed parameters"):
+        opt.swap_ema_weights(frozen)
+    with pytest.raises(ValueError, match="outside the optimizer"):
+        opt.swap_ema_weights(nn.Linear(4, 4).cuda())
+
+
+def test_cpu_staging_stays_out_of_the_checkpoint() -> None:
+    weights = _weights()
+    opt = _dion(weights, _config(EMADevice.CPU, 0.9))
+    _train(weights, opt)
+    for entry in opt.state_dict()["state"].values():
+        assert "ema_shadow" in entry
+        assert not {"ema_tmp_cpu", "ema_pending", "ema_event"} & set(entry)
+    assert "ema_tmp_cpu" in opt.state[weights[0]]
+
+
+@pytest.mark.parametrize(("saved_on", "loaded_on"), [(EMADevice.GPU, EMADevice.CPU),
+                                                     (EMADevice.CPU, EMADevice.GPU)])
+def test_checkpoint_moves_between_gpu_and_cpu_shadows(saved_on: EMADevice,
+                                                      loaded_on: EMADevice) -> None:
+    weights = _weights()
+    first = _dion(weights, _config(saved_on, 0.8))
+    _train(weights, first, steps=2)
+    second = _dion(weights, _config(loaded_on, 0.8))
+    # A deep copy stands for a save and load (torch's loader would keep tensors
+    # that already sit on the right device shared between the two optimizers).
+    second.load_state_dict(copy.deepcopy(first.state_dict()))
+    for w in weights:
+        assert _shadow(second, w).device.type == ("cuda" if loaded_on is EMADevice.GPU
+                                                   else "cpu")
+    g = torch.Generator().manual_seed(1)
+    grads = [torch.randn(w.shape, generator=g).cuda() for w in weights]
+    start = [w.detach().clone() for w in weights]
+    for opt in (first, second):
+        with torch.no_grad():
+            for w, x in zip(weights, start):
+                w.copy_(x)
+        for w, gr in zip(weights, grads):
+            w.grad = gr.clone()
+        opt.step()
+        # Both optimizers step the same weights: let a CPU snapshot finish
+        # reading them before the other optimizer overwrites them.
+        opt.ema.flush_pending_updates()
+    for w in weights:
+        assert torch.equal(_shadow(second, w).cuda(), _shadow(first, w).cuda())
+
+
+def test_ramped_decay_drives_each_update() -> None:
+    config = _config(EMADevice.GPU, 0.5, final=0.9, ramp=4)
+    weights = _weights()
+    opt = _dion(weights, config)
+    expected = None
+    for step in range(1, 7):
+        _train(weights, opt, seed=step)
+        live = [w.detach().clone() for w in weights]
+        expected = live if expected is None else [
+            e.lerp(x, 1 - config.decay_at_step(step)) for e, x in zip(expected, live)]
+    for w, e in zip(weights, expected):
+        torch.testing.assert_close(_shadow(opt, w), e, rtol=1e-6, atol=1e-6)
+
+
+class _TorchAdamWWithEMA(dionw.IntegratedEMAOptimizer, torch.optim.AdamW):
+    def __init__(self, params, ema: EMAConfig) -> None:
+        super().__init__(params, lr=1e-2)
+        self._init_integrated_ema(ema, no_profile)
+
+
+@pytest.mark.parametrize("device", list(EMADevice))
+def test_mixin_keeps_float32_shadows_of_bfloat16_weights(device: EMADevice) -> None:
+    g = torch.Generator().manual_seed(0)
+    w = nn.Parameter(torch.randn(64, 32, generator=g).to("cuda", torch.bfloat16))
+    opt = _TorchAdamWWithEMA([w], _config(device, 0.7))
+    expected = None
+    for _ in range(4):
+        w.grad = torch.randn(64, 32, generator=g).to("cuda", torch.bfloat16)
+        opt.step()
+        live = w.detach().float()
+        expected = live if expected is None else expected.lerp(live, 1 - 0.7)
+    opt.ema.flush_pending_updates()
+    shadow = opt.state[w]["ema_shadow"]
+    assert shadow.dtype == torch.float32
+    torch.testing.assert_close(shadow.cuda(), expected, rtol=1e-6, atol=1e-6)
