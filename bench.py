@@ -1,6 +1,6 @@
 """Benchmark of the Dion optimizer step on one MI355X.
 
-Default workload (BASELINE.json config 4): one full ``Dion.step()`` over
+Default workload: one full ``Dion.step()`` over
 Llama-3-8B-shaped float32 parameters — 32 layers of q/o 4096x4096, k/v
 1024x4096, gate/up 14336x4096, down 4096x14336 on Dion with fraction 0.25,
 embedding and lm_head 128256x4096 plus the RMSNorm weights on AdamW — with
@@ -137,7 +137,7 @@ def build_llama(torch, dev, spec, fraction):
 
 
 def build_gpt2(torch, dev):
-    """GPT-2 small. Every linear is Dion with fraction 0.25 and
+    """GPT-2 small (124 M parameters). Every linear is Dion with fraction 0.25 and
     selection_min_dim 1024, so with their 768-wide sides all update every row;
     LayerNorm weights/biases, linear biases, wte 50257x768 and wpe 1024x768 take AdamW."""
     g = torch.Generator(device=dev).manual_seed(0)
@@ -163,7 +163,7 @@ def build_gpt2(torch, dev):
 
 
 def build_moe(torch, dev):
-    """64 experts with fp32 gate/up 1408x2048 and down 2048x1408
+    """MoE expert stack: 64 experts with fp32 gate/up 1408x2048 and down 2048x1408
     (separate 2-D parameters), gradients 1e-3 * Student-t(df=3)."""
     g = torch.Generator(device=dev).manual_seed(0)
 
@@ -184,7 +184,7 @@ def build_moe(torch, dev):
 
 
 def gram_ns_bench(torch, steps: int, warmup: int) -> dict:
-    """standalone Gram Newton-Schulz on 16 bf16 blocks 1024x4096,
+    """Standalone Gram Newton-Schulz on 16 bf16 blocks 1024x4096,
     entries N(0,1) pre-normalized by their Frobenius norm, 5 iterations."""
     from dionw_amd.newton_schulz import NewtonSchulz, newton_schulz_fn
 

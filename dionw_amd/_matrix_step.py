@@ -51,9 +51,9 @@ NEWTON_SCHULZ_EPS: Final[float] = 1e-8
 # copy: a run keeps its selected rows in fp16 (row-major and transposed), the
 # bf16 output and the Newton-Schulz workspace (six fp16 r x r matrices and one
 # r x c per block): at most 20 bytes per update element (square blocks), under
-# 22 GB at this cap (17 GB for the Llama-3-8B gate/up bucket). Bigger runs fill the 256 CUs better (fewer partly idle tile
-# rounds per product) and launch fewer kernels; every Llama-3-8B bucket is
-# one run.
+# 22 GB at this cap (17 GB for the Llama-3-8B gate/up bucket). Bigger runs fill
+# the 256 CUs better (fewer partly idle tile rounds per product) and launch
+# fewer kernels; every Llama-3-8B bucket is one run.
 MAX_RUN_ELEMENTS: Final[int] = 2**30
 
 

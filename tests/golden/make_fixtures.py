@@ -8,7 +8,7 @@ package), so the vectors come from the oracle's restatement of its PyTorch path
   weight decay 0.1, Newton-Schulz replaced by the exact polar factor of the
   input (as tests/test_optimizer.py:90-132 does), so the GPU must match to
   float32 rounding; scores, indices, momentum, variance and weights per step.
-- ``config1.npz``: BASELINE config 1 — one step of a 1024x1024 fp32 weight
+- ``config1.npz``: one step of a 1024x1024 fp32 weight
   ~N(0, 0.02^2), gradient ~N(0, 1e-3^2), zero momentum, seed 0, fraction 1
   (NorMuon, the standard iteration of Gram Newton-Schulz on a square block),
   momentum 0.95, muon_beta2 0.95, lr 3e-4, weight decay 0.05: the variance, a
