@@ -60,7 +60,10 @@ def _dion(params, fraction, *, kind=NewtonSchulz.GRAM, weight_decay=0.0, normuon
 
 
 CASES = [((256, 512), 0.25), ((64, 128), 1.0), ((64, 128), 0.5), ((256, 64), 0.5),
-         ((128, 128), 0.25), ((160, 96), 1.0)]
+         ((128, 128), 0.25), ((160, 96), 1.0),
+         # sides that are not multiples of 8 or 4 (padded Newton-Schulz input,
+         # scalar row loads), and a long block (16384 rows, top-4096 selection)
+         ((100, 70), 0.3), ((37, 61), 1.0), ((16384, 128), 0.25)]
 
 
 @pytest.mark.parametrize("weight_decay", [0.0, 0.1])
@@ -97,9 +100,15 @@ def _exact_polar_cpu(x: torch.Tensor, epsilon: float) -> torch.Tensor:
 
 
 @pytest.mark.parametrize("kind", [NewtonSchulz.GRAM, NewtonSchulz.POLAR_EXPRESS, NewtonSchulz.KELLER_TRITON])
-@pytest.mark.parametrize(("shape", "fraction", "heads"), [((1024, 1024), 1.0, None), ((512, 1024), 0.25, None),
-                                                          ((768, 256), 1.0, 3), ((1408, 512), 0.25, None)])
-def test_hip_step_matches_oracle(kind, shape, fraction, heads) -> None:
+@pytest.mark.parametrize(("shape", "fraction", "heads", "bar"), [
+    ((1024, 1024), 1.0, None, 1e-2), ((512, 1024), 0.25, None, 1e-2), ((768, 256), 1.0, 3, 1e-2),
+    ((1408, 512), 0.25, None, 1e-2),
+    # 30 x 70 selected blocks (padded to 32 x 72): at this size the oracle's own
+    # fp16 Gram iteration is ~1e-2 from the float64 polynomial and bf16 Polar
+    # Express ~1.5e-2 (2.5e-3 and 1e-2 at 256 x 1024), so two independent
+    # roundings differ by up to ~1.5e-2.
+    ((100, 70), 0.3, None, 3e-2)])
+def test_hip_step_matches_oracle(kind, shape, fraction, heads, bar) -> None:
     """The full HIP step (Newton-Schulz included) against the oracle: selection
     and momentum bit-exact, the update within the Newton-Schulz rounding."""
     g = torch.Generator().manual_seed(1)
@@ -126,7 +135,7 @@ def test_hip_step_matches_oracle(kind, shape, fraction, heads) -> None:
         upd_gpu = param.detach().cpu().view(blocks, rows, cols) - before * decay
         upd_ref = w - w_ref_before * decay
         err = rel_fro(upd_gpu, upd_ref)
-        assert err < 1e-2, f"step {step} {kind.value} {shape}: update rel err {err}"
+        assert err < bar, f"step {step} {kind.value} {shape}: update rel err {err}"
         assert rel_fro(param.detach().cpu().view(blocks, rows, cols), w) < 2e-3
         got_v = opt.state[param]["variance"].cpu().view(blocks, rows, 1)
         assert rel_fro(got_v, var) < 2e-2, f"step {step}: variance"
