@@ -106,8 +106,18 @@ class Timeline:
                 n = count * bpt * rows * cols
                 s = count * bpt * k * cols
                 entry["bytes"] += (8.0 * n if decay_on else 8.0 * s) + 2.0 * s
+            elif name == "dionw_apply_update_ema":
+                # every row: W read, S read and written; W written where it changes
+                count, bpt, rows, cols, k, decay_on = a[2], a[3], a[4], a[5], a[6], a[14]
+                n = count * bpt * rows * cols
+                s = count * bpt * k * cols
+                entry["bytes"] += 12.0 * n + (4.0 * n if decay_on else 4.0 * s) + 2.0 * s
             elif name == "dionw_adamw":
                 entry["bytes"] += 28.0 * sum(a[5][i] for i in range(a[6]))
+            elif name == "dionw_adamw_ema":
+                entry["bytes"] += 36.0 * sum(a[6][i] for i in range(a[7]))
+            elif name == "dionw_ema_update":
+                entry["bytes"] += (8.0 if a[5] else 12.0) * sum(a[2][i] for i in range(a[3]))
         return dict(out)
 
 

@@ -16,6 +16,7 @@ from torch import Tensor
 from dionw_amd import _lib
 from dionw_amd._keys import ADAMW_STEP_STATE, EXP_AVG_SQ_STATE, EXP_AVG_STATE, ParamState
 from dionw_amd._layout import same_dense_layout
+from dionw_amd.ema._fusion import ACTIVE_EMA
 
 __all__ = ["adamw_step", "init_adamw_state"]
 
@@ -68,22 +69,20 @@ def adamw_step(group: dict[str, Any], state: ParamState) -> None:
     stream = _lib.stream_handle(params[0].device)
     _lib.call("dionw_increment_steps", _lib.ptr_array(steps), len(steps), stream)
     beta1, beta2 = group["betas"]
-    _lib.call(
-        "dionw_adamw",
-        _lib.ptr_array(targets),
-        _lib.ptr_array(grads),
-        _lib.ptr_array(exp_avgs),
-        _lib.ptr_array(exp_avg_sqs),
-        _lib.ptr_array(steps),
-        _lib.int64_array([t.numel() for t in targets]),
-        len(targets),
-        float(group["lr"]),
-        float(beta1),
-        float(beta2),
-        float(group["weight_decay"]),
-        float(group["eps"]),
-        stream,
-    )
+    tensors = (_lib.ptr_array(targets), _lib.ptr_array(grads), _lib.ptr_array(exp_avgs),
+               _lib.ptr_array(exp_avg_sqs), _lib.ptr_array(steps))
+    sizes = (_lib.int64_array([t.numel() for t in targets]), len(targets))
+    scalars = (float(group["lr"]), float(beta1), float(beta2), float(group["weight_decay"]),
+               float(group["eps"]))
+    # A due GPU EMA lerp of these parameters rides on the AdamW pass.
+    ema = ACTIVE_EMA.get()
+    shadows = ema.fusable_shadows(params) if ema is not None and not copies else None
+    if shadows is None:
+        _lib.call("dionw_adamw", *tensors, *sizes, *scalars, stream)
+    else:
+        _lib.call("dionw_adamw_ema", *tensors, _lib.ptr_array(shadows), *sizes, *scalars,
+                  ema.fused_weight(), stream)
+        ema.mark_fused(params)
     for original, copy in copies:
         if original.data_ptr() != copy.data_ptr():
             original.copy_(copy)

@@ -79,10 +79,18 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [_pp, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _f32, _f32, _i32, _p],
     ),
+    "dionw_apply_update_ema": (
+        ctypes.c_int,
+        [_pp, _pp, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _f32, _f32, _i32, _f32, _p],
+    ),
     "dionw_increment_steps": (ctypes.c_int, [_pp, _i32, _p]),
     "dionw_adamw": (
         ctypes.c_int,
         [_pp, _pp, _pp, _pp, _pp, _pi64, _i32, _f64, _f64, _f64, _f64, _f64, _p],
+    ),
+    "dionw_adamw_ema": (
+        ctypes.c_int,
+        [_pp, _pp, _pp, _pp, _pp, _pp, _pi64, _i32, _f64, _f64, _f64, _f64, _f64, _f32, _p],
     ),
     "dionw_ema_update": (ctypes.c_int, [_pp, _pp, _pi64, _i32, _f32, _i32, _p]),
 }

@@ -13,7 +13,8 @@ Reference: src/dionw/_matrix_step.py:104-311. Per block:
 On the HIP path this is five to seven launches per run, each over the whole
 run through pointer tables: accumulate/sumsq, select, prepare (decay + the
 normalized 16-bit input in both orientations), the Newton-Schulz products,
-NorMuon statistics and the fused apply. A user-supplied orthogonalization
+NorMuon statistics and the fused apply (which also takes a due GPU EMA lerp of
+the run's weights). A user-supplied orthogonalization
 (``newton_schulz_fn`` replaced) receives the float32 input rows instead, as
 the reference's plugin does.
 """
@@ -36,6 +37,7 @@ from dionw_amd._keys import (
     ROW_NORMALIZATION_KEY,
     ParamState,
 )
+from dionw_amd.ema._fusion import ACTIVE_EMA
 from dionw_amd.matrix_update import MomentumForm, RowNormalization
 from dionw_amd.newton_schulz import HipOrthogonalize, run_newton_schulz
 
@@ -190,10 +192,19 @@ def step_run(
 
     weight_decay = float(group["weight_decay"])
     decay = 1.0 - lr * weight_decay
-    _lib.call("dionw_apply_update", _lib.ptr_array(run.params), count, per_param, rows, cols, k,
-              orthogonal.data_ptr(), idx_ptr, None if slot is None else slot.data_ptr(),
-              None if rowd is None else rowd.data_ptr(),
-              None if scale is None else scale.data_ptr(), step, decay,
-              int(weight_decay > 0.0), stream)
+    common = (count, per_param, rows, cols, k, orthogonal.data_ptr(), idx_ptr,
+              None if slot is None else slot.data_ptr(), None if rowd is None else rowd.data_ptr(),
+              None if scale is None else scale.data_ptr(), step, decay, int(weight_decay > 0.0))
+    # A due GPU EMA lerp of these weights rides on the apply pass (one pass
+    # instead of apply then EMA; the same lerp arithmetic).
+    ema = ACTIVE_EMA.get()
+    params = [bucket.params[i] for i in positions]
+    shadows = ema.fusable_shadows(params) if ema is not None and not run.writeback else None
+    if shadows is None:
+        _lib.call("dionw_apply_update", _lib.ptr_array(run.params), *common, stream)
+    else:
+        _lib.call("dionw_apply_update_ema", _lib.ptr_array(run.params), _lib.ptr_array(shadows),
+                  *common, ema.fused_weight(), stream)
+        ema.mark_fused(params)
     for param, copy in run.writeback:
         param.copy_(copy)

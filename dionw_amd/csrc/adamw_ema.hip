@@ -23,6 +23,7 @@ struct AdamTable {
   float* m[kMaxAdam];
   float* v[kMaxAdam];
   const float* step[kMaxAdam];
+  float* shadow[kMaxAdam];  // EMA shadows updated from the new parameters (fused EMA)
   int64_t numel[kMaxAdam];
   int32_t chunk0[kMaxAdam + 1];  // first chunk of each tensor
   int count;
@@ -65,7 +66,8 @@ __device__ __forceinline__ void adamw_element(float& param_io, float grad, float
   exp_avg_sq_io = exp_avg_sq;
 }
 
-__global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s) {
+template <bool EMA>
+__global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s, float ema_weight) {
   const int tensor = find_tensor(t.chunk0, t.count, blockIdx.x);
   const int64_t local = (int64_t)(blockIdx.x - t.chunk0[tensor]) * kChunk;
   const int64_t n = t.numel[tensor] - local;
@@ -77,8 +79,10 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s) 
   const float* g = t.g[tensor] + local;
   float* m = t.m[tensor] + local;
   float* v = t.v[tensor] + local;
+  float* sh = EMA ? t.shadow[tensor] + local : nullptr;
   const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
-                     reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
+                     reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v) |
+                     reinterpret_cast<uintptr_t>(sh)) & 15) == 0;
   int64_t i = 0;
   if (vec) {
     f32x4* p4 = reinterpret_cast<f32x4*>(p);
@@ -97,6 +101,13 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s) 
       p4[q] = pv;
       m4[q] = mv;
       v4[q] = vv;
+      if (EMA) {
+        f32x4* s4 = reinterpret_cast<f32x4*>(sh);
+        f32x4 sv = s4[q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], pv[e], ema_weight);
+        s4[q] = sv;
+      }
     };
     const int64_t n4 = end >> 2;
     int64_t q = threadIdx.x;
@@ -118,6 +129,7 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s) 
     p[e] = pe;
     m[e] = me;
     v[e] = ve;
+    if (EMA) sh[e] = ema_lerp(sh[e], pe, ema_weight);
   }
 }
 
@@ -141,11 +153,6 @@ struct EmaTable {
   int count;
 };
 
-__device__ __forceinline__ float lerp_scalar(float self, float end, float weight) {
-  return fabsf(weight) < 0.5f ? self + weight * (end - self)
-                              : end - (end - self) * (1.f - weight);
-}
-
 template <bool COPY>
 __global__ __launch_bounds__(256) void ema_kernel(EmaTable t, float weight) {
   const int tensor = find_tensor(t.chunk0, t.count, blockIdx.x);
@@ -164,14 +171,56 @@ __global__ __launch_bounds__(256) void ema_kernel(EmaTable t, float weight) {
       } else {
         f32x4 sv = reinterpret_cast<f32x4*>(s)[q];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sv[e] = lerp_scalar(sv[e], pv[e], weight);
+        for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], pv[e], weight);
         reinterpret_cast<f32x4*>(s)[q] = sv;
       }
     }
     i = end & ~(int64_t)3;
   }
   for (int64_t e = i + threadIdx.x; e < end; e += 256)
-    s[e] = COPY ? p[e] : lerp_scalar(s[e], p[e], weight);
+    s[e] = COPY ? p[e] : ema_lerp(s[e], p[e], weight);
+}
+
+// One launch per kMaxAdam tensors; shadows (may be null) get the fused EMA lerp.
+int adamw_launch(float* const* params, const float* const* grads, float* const* exp_avgs,
+                 float* const* exp_avg_sqs, const float* const* steps, float* const* shadows,
+                 const int64_t* numels, int32_t count, const AdamScalars& s, float ema_weight,
+                 hipStream_t stream) {
+  for (int32_t start = 0; start < count;) {
+    AdamTable t{};
+    int32_t chunks = 0;
+    while (start < count && t.count < kMaxAdam) {
+      const int i = start;
+      DIONW_REQUIRE(params[i] && grads[i] && exp_avgs[i] && exp_avg_sqs[i] && steps[i],
+                    "adamw: null pointer in tensor %d", i);
+      DIONW_REQUIRE(!shadows || shadows[i], "adamw: null EMA shadow in tensor %d", i);
+      DIONW_REQUIRE(numels[i] >= 0, "adamw: negative numel");
+      const int64_t c = ceil_div(numels[i], kChunk);
+      if ((int64_t)chunks + c > INT32_MAX / 2) break;
+      ++start;
+      if (c == 0) continue;
+      t.p[t.count] = params[i];
+      t.g[t.count] = grads[i];
+      t.m[t.count] = exp_avgs[i];
+      t.v[t.count] = exp_avg_sqs[i];
+      t.step[t.count] = steps[i];
+      t.shadow[t.count] = shadows ? shadows[i] : nullptr;
+      t.numel[t.count] = numels[i];
+      t.chunk0[t.count] = chunks;
+      chunks += (int32_t)c;
+      ++t.count;
+    }
+    if (t.count == 0) continue;
+    t.chunk0[t.count] = chunks;
+    if (shadows)
+      hipLaunchKernelGGL(adamw_kernel<true>, dim3((unsigned)chunks), dim3(256), 0, stream, t, s,
+                         ema_weight);
+    else
+      hipLaunchKernelGGL(adamw_kernel<false>, dim3((unsigned)chunks), dim3(256), 0, stream, t, s,
+                         0.f);
+    DIONW_TRY(check_launch("adamw"));
+  }
+  return kOk;
 }
 
 }  // namespace
@@ -199,35 +248,17 @@ int dionw_adamw(float* const* params, const float* const* grads, float* const* e
                 float* const* exp_avg_sqs, const float* const* steps, const int64_t* numels,
                 int32_t count, double lr, double beta1, double beta2, double weight_decay,
                 double eps, hipStream_t stream) {
-  AdamScalars s{lr, beta1, beta2, weight_decay, eps};
-  for (int32_t start = 0; start < count;) {
-    AdamTable t{};
-    int32_t chunks = 0;
-    while (start < count && t.count < kMaxAdam) {
-      const int i = start;
-      DIONW_REQUIRE(params[i] && grads[i] && exp_avgs[i] && exp_avg_sqs[i] && steps[i],
-                    "adamw: null pointer in tensor %d", i);
-      DIONW_REQUIRE(numels[i] >= 0, "adamw: negative numel");
-      const int64_t c = ceil_div(numels[i], kChunk);
-      if ((int64_t)chunks + c > INT32_MAX / 2) break;
-      ++start;
-      if (c == 0) continue;
-      t.p[t.count] = params[i];
-      t.g[t.count] = grads[i];
-      t.m[t.count] = exp_avgs[i];
-      t.v[t.count] = exp_avg_sqs[i];
-      t.step[t.count] = steps[i];
-      t.numel[t.count] = numels[i];
-      t.chunk0[t.count] = chunks;
-      chunks += (int32_t)c;
-      ++t.count;
-    }
-    if (t.count == 0) continue;
-    t.chunk0[t.count] = chunks;
-    hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)chunks), dim3(256), 0, stream, t, s);
-    DIONW_TRY(check_launch("adamw"));
-  }
-  return kOk;
+  return adamw_launch(params, grads, exp_avgs, exp_avg_sqs, steps, nullptr, numels, count,
+                      AdamScalars{lr, beta1, beta2, weight_decay, eps}, 0.f, stream);
+}
+
+int dionw_adamw_ema(float* const* params, const float* const* grads, float* const* exp_avgs,
+                    float* const* exp_avg_sqs, const float* const* steps, float* const* shadows,
+                    const int64_t* numels, int32_t count, double lr, double beta1, double beta2,
+                    double weight_decay, double eps, float ema_weight, hipStream_t stream) {
+  DIONW_REQUIRE(shadows, "adamw_ema: null shadow table");
+  return adamw_launch(params, grads, exp_avgs, exp_avg_sqs, steps, shadows, numels, count,
+                      AdamScalars{lr, beta1, beta2, weight_decay, eps}, ema_weight, stream);
 }
 
 int dionw_ema_update(float* const* shadows, const float* const* sources, const int64_t* numels,

@@ -64,6 +64,16 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
+// torch's lerp, as the EMA uses it (ATen Lerp.h: |w| < 0.5 ? self + w (end -
+// self) : end - (end - self)(1 - w)), with the multiply-adds fused the way
+// hipcc fuses them under its default contraction; spelled out so every kernel
+// that updates a shadow rounds identically whatever its file's contraction mode.
+__device__ __forceinline__ float ema_lerp(float self, float end, float weight) {
+  const float diff = end - self;
+  return fabsf(weight) < 0.5f ? __builtin_fmaf(weight, diff, self)
+                              : __builtin_fmaf(-diff, 1.f - weight, end);
+}
+
 // Rounding to the 16-bit storage types (round to nearest even).
 __device__ __forceinline__ _Float16 to_f16(float x) { return (_Float16)x; }
 __device__ __forceinline__ __bf16 to_bf16(float x) { return (__bf16)x; }

@@ -96,6 +96,8 @@ struct ApplyArgs {
   float step, decay;
   int apply_decay, only_selected, vec;
   int64_t rows_per_tensor, rows, cols, k;
+  float* shadow[kMaxTensors];  // EMA shadows laid out like the parameters (fused EMA)
+  float ema_weight;
 };
 
 __device__ __forceinline__ float update_one(float w, float o, float d, float s,
@@ -109,6 +111,9 @@ __device__ __forceinline__ float update_one(float w, float o, float d, float s,
 // faster than a wavefront per row).
 constexpr int kApplyThreads = 256;
 
+// EMA: every row's shadow also moves to the row's new weights (lerp with
+// ema_weight), also on rows that are only decayed or not changed at all.
+template <bool EMA>
 __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
   const int tid = threadIdx.x;
   const int64_t r = blockIdx.x;  // the grid has exactly one workgroup per row
@@ -124,14 +129,31 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
     slot = a.slot ? (int64_t)a.slot[b * a.rows + in_block] : in_block;
   }
   const int tensor = (int)(gr / a.rows_per_tensor);
-  float* w = a.t.param[tensor] + (gr - (int64_t)tensor * a.rows_per_tensor) * a.cols;
+  const int64_t offset = (gr - (int64_t)tensor * a.rows_per_tensor) * a.cols;
+  float* w = a.t.param[tensor] + offset;
+  float* sh = EMA ? a.shadow[tensor] + offset : nullptr;
   const bool apply_decay = a.apply_decay != 0;
   constexpr int U = 4;  // chunks whose loads are issued together
   constexpr int T = kApplyThreads;
   if (slot < 0) {
-    if (!apply_decay) return;
+    if (!apply_decay && !EMA) return;
+    // Rows outside the selection: W = W d (weight decay) and, with the EMA,
+    // S = lerp(S, W).
+    auto row_end = [&](f32x4 wv, int64_t c) {
+      if (apply_decay) {
+        wv = wv * a.decay;
+        reinterpret_cast<f32x4*>(w)[c] = wv;
+      }
+      if (EMA) {
+        f32x4* s4 = reinterpret_cast<f32x4*>(sh);
+        f32x4 sv = s4[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], wv[e], a.ema_weight);
+        s4[c] = sv;
+      }
+    };
     if (a.vec) {
-      f32x4* w4 = reinterpret_cast<f32x4*>(w);
+      const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
       const int64_t n4 = a.cols >> 2;
       int64_t c = tid;
       for (; c + (U - 1) * T < n4; c += U * T) {
@@ -139,11 +161,15 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) wv[u] = w4[c + u * T];
 #pragma unroll
-        for (int u = 0; u < U; ++u) w4[c + u * T] = wv[u] * a.decay;
+        for (int u = 0; u < U; ++u) row_end(wv[u], c + u * T);
       }
-      for (; c < n4; c += T) w4[c] = w4[c] * a.decay;
+      for (; c < n4; c += T) row_end(w4[c], c);
     } else {
-      for (int64_t c = tid; c < a.cols; c += T) w[c] = w[c] * a.decay;
+      for (int64_t c = tid; c < a.cols; c += T) {
+        float wv = w[c];
+        if (apply_decay) w[c] = wv = wv * a.decay;
+        if (EMA) sh[c] = ema_lerp(sh[c], wv, a.ema_weight);
+      }
     }
     return;
   }
@@ -161,6 +187,16 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
         wv[e] = update_one(wv[e], (float)ov[e], d, s, normalized, a.decay, apply_decay);
       return wv;
     };
+    auto store = [&](int64_t c, f32x4 wv) {
+      w4[c] = wv;
+      if (EMA) {
+        f32x4* s4 = reinterpret_cast<f32x4*>(sh);
+        f32x4 sv = s4[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], wv[e], a.ema_weight);
+        s4[c] = sv;
+      }
+    };
     const int64_t n4 = a.cols >> 2;
     int64_t c = tid;
     for (; c + (U - 1) * T < n4; c += U * T) {
@@ -172,13 +208,71 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
         ov[u] = o4[c + u * T];
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) w4[c + u * T] = upd(wv[u], ov[u]);
+      for (int u = 0; u < U; ++u) store(c + u * T, upd(wv[u], ov[u]));
     }
-    for (; c < n4; c += T) w4[c] = upd(w4[c], o4[c]);
+    for (; c < n4; c += T) store(c, upd(w4[c], o4[c]));
   } else {
-    for (int64_t c = tid; c < a.cols; c += T)
-      w[c] = update_one(w[c], (float)o[c], d, s, normalized, a.decay, apply_decay);
+    for (int64_t c = tid; c < a.cols; c += T) {
+      const float wv = update_one(w[c], (float)o[c], d, s, normalized, a.decay, apply_decay);
+      w[c] = wv;
+      if (EMA) sh[c] = ema_lerp(sh[c], wv, a.ema_weight);
+    }
   }
+}
+
+// One launch per kMaxTensors parameters; shadows (may be null) get the fused EMA.
+int apply_launch(float* const* params, float* const* shadows, int32_t count,
+                 int64_t blocks_per_tensor, int64_t rows, int64_t cols, int64_t k,
+                 const void* orthogonal, const int32_t* idx, const int32_t* slot,
+                 const float* rowd, const float* scale, float step, float decay,
+                 int32_t apply_decay, float ema_weight, hipStream_t stream) {
+  DIONW_REQUIRE(orthogonal && count >= 0 && blocks_per_tensor > 0 && rows > 0 && cols > 0 &&
+                    k > 0 && k <= rows,
+                "apply_update: bad arguments");
+  DIONW_REQUIRE(k == rows || (idx && slot), "apply_update: row selection needs idx and slot");
+  for (int32_t start = 0; start < count; start += kMaxTensors) {
+    ApplyArgs a{};
+    a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
+    bool aligned = cols % 4 == 0;
+    for (int i = 0; i < a.t.count; ++i) {
+      DIONW_REQUIRE(params[start + i], "apply_update: null parameter %d", start + i);
+      a.t.param[i] = params[start + i];
+      aligned = aligned && aligned16(params[start + i]);
+      if (shadows) {
+        DIONW_REQUIRE(shadows[start + i], "apply_update: null EMA shadow %d", start + i);
+        a.shadow[i] = shadows[start + i];
+        aligned = aligned && aligned16(shadows[start + i]);
+      }
+    }
+    const int64_t b0 = (int64_t)start * blocks_per_tensor;
+    a.o = reinterpret_cast<const __bf16*>(orthogonal) + b0 * k * cols;
+    a.idx = idx ? idx + b0 * k : nullptr;
+    a.slot = (slot && k < rows) ? slot + b0 * rows : nullptr;
+    a.rowd = rowd ? rowd + b0 * k : nullptr;
+    a.scale = scale ? scale + b0 : nullptr;
+    a.step = step;
+    a.decay = decay;
+    a.apply_decay = apply_decay;
+    a.rows_per_tensor = blocks_per_tensor * rows;
+    a.rows = rows;
+    a.cols = cols;
+    a.k = k;
+    a.vec = aligned && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;
+    a.ema_weight = ema_weight;
+    // The EMA moves every row's shadow, so every row is visited.
+    a.only_selected = !apply_decay && !shadows && k < rows;
+    const int64_t n = a.only_selected ? (int64_t)a.t.count * blocks_per_tensor * k
+                                      : (int64_t)a.t.count * a.rows_per_tensor;
+    if (n == 0) continue;
+    DIONW_REQUIRE(n * kApplyThreads <= (int64_t)UINT32_MAX,
+                  "apply_update: %lld rows exceed one launch", (long long)n);
+    if (shadows)
+      hipLaunchKernelGGL(apply_kernel<true>, dim3((unsigned)n), dim3(kApplyThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL(apply_kernel<false>, dim3((unsigned)n), dim3(kApplyThreads), 0, stream, a);
+    DIONW_TRY(check_launch("apply_update"));
+  }
+  return kOk;
 }
 
 }  // namespace
@@ -222,43 +316,18 @@ int dionw_apply_update(float* const* params, int32_t count, int64_t blocks_per_t
                        const int32_t* idx, const int32_t* slot, const float* rowd,
                        const float* scale, float step, float decay, int32_t apply_decay,
                        hipStream_t stream) {
-  DIONW_REQUIRE(orthogonal && count >= 0 && blocks_per_tensor > 0 && rows > 0 && cols > 0 &&
-                    k > 0 && k <= rows,
-                "apply_update: bad arguments");
-  DIONW_REQUIRE(k == rows || (idx && slot), "apply_update: row selection needs idx and slot");
-  for (int32_t start = 0; start < count; start += kMaxTensors) {
-    ApplyArgs a{};
-    a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
-    bool aligned = cols % 4 == 0;
-    for (int i = 0; i < a.t.count; ++i) {
-      DIONW_REQUIRE(params[start + i], "apply_update: null parameter %d", start + i);
-      a.t.param[i] = params[start + i];
-      aligned = aligned && aligned16(params[start + i]);
-    }
-    const int64_t b0 = (int64_t)start * blocks_per_tensor;
-    a.o = reinterpret_cast<const __bf16*>(orthogonal) + b0 * k * cols;
-    a.idx = idx ? idx + b0 * k : nullptr;
-    a.slot = (slot && k < rows) ? slot + b0 * rows : nullptr;
-    a.rowd = rowd ? rowd + b0 * k : nullptr;
-    a.scale = scale ? scale + b0 : nullptr;
-    a.step = step;
-    a.decay = decay;
-    a.apply_decay = apply_decay;
-    a.rows_per_tensor = blocks_per_tensor * rows;
-    a.rows = rows;
-    a.cols = cols;
-    a.k = k;
-    a.vec = aligned && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;
-    a.only_selected = !apply_decay && k < rows;
-    const int64_t n = a.only_selected ? (int64_t)a.t.count * blocks_per_tensor * k
-                                      : (int64_t)a.t.count * a.rows_per_tensor;
-    if (n == 0) continue;
-    DIONW_REQUIRE(n * kApplyThreads <= (int64_t)UINT32_MAX,
-                  "apply_update: %lld rows exceed one launch", (long long)n);
-    hipLaunchKernelGGL(apply_kernel, dim3((unsigned)n), dim3(kApplyThreads), 0, stream, a);
-    DIONW_TRY(check_launch("apply_update"));
-  }
-  return kOk;
+  return apply_launch(params, nullptr, count, blocks_per_tensor, rows, cols, k, orthogonal, idx,
+                      slot, rowd, scale, step, decay, apply_decay, 0.f, stream);
+}
+
+int dionw_apply_update_ema(float* const* params, float* const* shadows, int32_t count,
+                           int64_t blocks_per_tensor, int64_t rows, int64_t cols, int64_t k,
+                           const void* orthogonal, const int32_t* idx, const int32_t* slot,
+                           const float* rowd, const float* scale, float step, float decay,
+                           int32_t apply_decay, float ema_weight, hipStream_t stream) {
+  DIONW_REQUIRE(shadows, "apply_update_ema: null shadow table");
+  return apply_launch(params, shadows, count, blocks_per_tensor, rows, cols, k, orthogonal, idx,
+                      slot, rowd, scale, step, decay, apply_decay, ema_weight, stream);
 }
 
 }  // extern "C"

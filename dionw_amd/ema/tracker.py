@@ -3,7 +3,9 @@
 Reference: src/dionw/ema/tracker.py:40-299. GPU shadows are queued during the
 step and updated at ``finalize_updates`` by the multi-tensor HIP kernels
 (copies for shadows not yet initialized, lerps for the rest), with no host
-synchronization. CPU shadows receive a snapshot copied on a side stream into
+synchronization; a Dion step may instead take the lerp of the parameters it
+writes into its own apply and AdamW passes (``fusable_shadows``), which then
+skip the queue. CPU shadows receive a snapshot copied on a side stream into
 pinned buffers, then a background thread applies the update (one job in
 flight at most).
 """
@@ -56,6 +58,8 @@ class OptimizerIntegratedEMA:
         self._copy_streams: dict[torch.device, torch.cuda.Stream] = {}
         self._gpu_copy: tuple[list[Tensor], list[Tensor]] = ([], [])
         self._gpu_lerp: tuple[list[Tensor], list[Tensor]] = ([], [])
+        # Parameters whose update of this step the optimizer's own pass took.
+        self._fused: set[int] = set()
 
     # -- schedule ------------------------------------------------------------
     @property
@@ -76,6 +80,7 @@ class OptimizerIntegratedEMA:
 
     def begin_step(self) -> None:
         """Advance the schedule at the start of an optimizer step."""
+        self._fused.clear()
         if not self._use_gpu_shadow:
             self._wait_for_previous_snapshot_copy()
         self._step_count += 1
@@ -99,6 +104,39 @@ class OptimizerIntegratedEMA:
         """Whether this step updates the shadows."""
         return self._do_update
 
+    # -- fusion into the optimizer's passes ------------------------------------
+    def fusable_shadows(self, params: list[Tensor]) -> list[Tensor] | None:
+        """The shadows of ``params`` if this step's update of every one of them
+        is a GPU lerp that the optimizer may apply in its own pass over the new
+        weights (initialized float32 shadows laid out like their contiguous
+        float32 parameters), else None."""
+        if not (self._use_gpu_shadow and self._do_update) or self._initialize_from_live:
+            return None
+        shadows = []
+        for param in params:
+            state = self.optimizer.state.get(param)
+            shadow = state.get(EMA_SHADOW) if state else None
+            if (
+                shadow is None
+                or not state.get(EMA_INITIALIZED, False)
+                or param.dtype != FP32
+                or shadow.shape != param.shape
+                or shadow.device != param.device
+                or not (param.is_contiguous() and shadow.is_contiguous())
+            ):
+                return None
+            shadows.append(shadow)
+        return shadows
+
+    def fused_weight(self) -> float:
+        """The lerp weight of this step's update (as foreach_ema_update_ forms it)."""
+        decay = self.config.decay if self._eff_decay is None else self._eff_decay
+        return 1.0 - decay
+
+    def mark_fused(self, params: list[Tensor]) -> None:
+        """Record that the optimizer's pass updated these parameters' shadows."""
+        self._fused.update(id(param) for param in params)
+
     # -- queueing ------------------------------------------------------------
     def _create_shadow(self, param: Tensor, state: dict[str, Any]) -> None:
         if self._use_gpu_shadow and not param.is_cuda:
@@ -117,6 +155,9 @@ class OptimizerIntegratedEMA:
             if not self._do_update or param not in self.optimizer.state:
                 return
             state = self.optimizer.state[param]
+            if id(param) in self._fused:
+                state[EMA_PENDING] = False
+                return
             if EMA_SHADOW not in state:
                 self._create_shadow(param, state)
             if self._use_gpu_shadow:
@@ -173,6 +214,7 @@ class OptimizerIntegratedEMA:
         with self._profile_region(_FINALIZE_REGION):
             if self._use_gpu_shadow:
                 self._finalize_gpu_updates()
+                self._fused.clear()
                 return
             if not self._do_update:
                 return

@@ -34,6 +34,7 @@ from dionw_amd._keys import (
     STRUCTURAL_KEYS,
 )
 from dionw_amd._matrix_step import MAX_RUN_ELEMENTS, run_elements, step_run
+from dionw_amd.ema._fusion import ACTIVE_EMA
 from dionw_amd.ema import EMAConfig, IntegratedEMAOptimizer, ProfileRegion, no_profile
 from dionw_amd.matrix_update import DION3_UPDATE, MatrixUpdate, MomentumForm, RowNormalization
 from dionw_amd.newton_schulz import NewtonSchulz
@@ -214,11 +215,16 @@ class _DionCore(Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        for bucket in self._ensure_buckets():
-            self._step_bucket(bucket)
-        for group in self.param_groups:
-            if RouteKind(group[ROUTE_KEY]) is RouteKind.ADAMW:
-                adamw_step(group, self.state)
+        # A due GPU EMA update can ride on the passes that write the new weights.
+        token = ACTIVE_EMA.set(getattr(self, "ema", None))
+        try:
+            for bucket in self._ensure_buckets():
+                self._step_bucket(bucket)
+            for group in self.param_groups:
+                if RouteKind(group[ROUTE_KEY]) is RouteKind.ADAMW:
+                    adamw_step(group, self.state)
+        finally:
+            ACTIVE_EMA.reset(token)
         return loss
 
     def _ensure_buckets(self) -> list[Bucket]:

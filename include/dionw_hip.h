@@ -161,6 +161,21 @@ int dionw_apply_update(float* const* params, int32_t count, int64_t blocks_per_t
                        const float* scale, float step, float decay, int32_t apply_decay,
                        dionw_stream_t stream);
 
+/*
+ * dionw_apply_update with the GPU EMA fused in: after a row's new weights are
+ * formed, its float32 shadow (same layout as the parameter, shadows[i] for
+ * params[i]) becomes lerp(shadow, W_new, ema_weight), on every row (also those
+ * only decayed or unchanged). Replaces the apply pass followed by
+ * foreach_ema_update_ over the same parameters (_matrix_step.py:274-311, then
+ * ema/_update.py:32-70 from ema/tracker.py:217-227) with one pass: 4 bytes per
+ * element less than the two.
+ */
+int dionw_apply_update_ema(float* const* params, float* const* shadows, int32_t count,
+                           int64_t blocks_per_tensor, int64_t rows, int64_t cols, int64_t k,
+                           const void* orthogonal, const int32_t* idx, const int32_t* slot,
+                           const float* rowd, const float* scale, float step, float decay,
+                           int32_t apply_decay, float ema_weight, dionw_stream_t stream);
+
 /* steps[i] += 1 (float32 device scalars): the _foreach_add_ of _adamw.py:47. */
 int dionw_increment_steps(float* const* steps, int32_t count, dionw_stream_t stream);
 
@@ -173,6 +188,17 @@ int dionw_adamw(float* const* params, const float* const* grads, float* const* e
                 float* const* exp_avg_sqs, const float* const* steps, const int64_t* numels,
                 int32_t count, double lr, double beta1, double beta2, double weight_decay,
                 double eps, dionw_stream_t stream);
+
+/*
+ * dionw_adamw with the GPU EMA fused in: shadows[i] = lerp(shadows[i], new
+ * params[i], ema_weight). Replaces _fused_adamw_ followed by
+ * foreach_ema_update_ over the same tensors (_adamw.py:45-61, then
+ * ema/_update.py:32-70 from ema/tracker.py:217-227) with one pass.
+ */
+int dionw_adamw_ema(float* const* params, const float* const* grads, float* const* exp_avgs,
+                    float* const* exp_avg_sqs, const float* const* steps, float* const* shadows,
+                    const int64_t* numels, int32_t count, double lr, double beta1, double beta2,
+                    double weight_decay, double eps, float ema_weight, dionw_stream_t stream);
 
 /*
  * GPU EMA of float32 sources: shadow = lerp(shadow, source, weight), or a

@@ -244,3 +244,55 @@ def test_mixin_keeps_float32_shadows_of_bfloat16_weights(device: EMADevice) -> N
     shadow = opt.state[w]["ema_shadow"]
     assert shadow.dtype == torch.float32
     torch.testing.assert_close(shadow.cuda(), expected, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("weight_decay", [0.0, 0.1])
+@pytest.mark.parametrize("every", [1, 2])
+def test_fused_ema_equals_the_separate_pass(weight_decay: float, every: int,
+                                           monkeypatch: pytest.MonkeyPatch) -> None:
+    """The shadow lerp taken inside the apply and AdamW passes is bit-identical
+    to the separate EMA pass (same lerp arithmetic on the same new weights), on
+    selected, decay-only and unchanged rows alike."""
+    from dionw_amd import _lib
+    from dionw_amd.ema.tracker import OptimizerIntegratedEMA
+
+    def build():
+        g = torch.Generator().manual_seed(3)
+        weights = [nn.Parameter(torch.randn(64, 96, generator=g).cuda()),   # selected rows
+                   nn.Parameter(torch.randn(32, 48, generator=g).cuda()),   # every row
+                   nn.Parameter(torch.randn(96, generator=g).cuda())]       # AdamW
+        opt = dionw.Dion(
+            [{"params": [weights[0]], dionw.ROUTE_KEY: "matrix", dionw.FRACTION_KEY: 0.25},
+             {"params": [weights[1]], dionw.ROUTE_KEY: "matrix", dionw.FRACTION_KEY: 1.0},
+             {"params": [weights[2]], dionw.ROUTE_KEY: "adamw"}],
+            lr=1e-2, weight_decay=weight_decay, ema=_config(EMADevice.GPU, 0.9, every=every))
+        return weights, opt
+
+    def run(fuse: bool):
+        names: list[str] = []
+        original = _lib.call
+
+        def recording(name, *args):
+            names.append(name)
+            return original(name, *args)
+
+        with monkeypatch.context() as m:
+            m.setattr(_lib, "call", recording)
+            if not fuse:
+                m.setattr(OptimizerIntegratedEMA, "fusable_shadows", lambda self, params: None)
+            weights, opt = build()
+            g = torch.Generator().manual_seed(4)
+            for _ in range(5):
+                for w in weights:
+                    w.grad = torch.randn(w.shape, generator=g).cuda()
+                opt.step()
+            opt.ema.flush_pending_updates()
+        return weights, opt, names
+
+    fused_w, fused_opt, fused_names = run(True)
+    plain_w, plain_opt, plain_names = run(False)
+    assert "dionw_apply_update_ema" in fused_names and "dionw_adamw_ema" in fused_names
+    assert "dionw_apply_update_ema" not in plain_names
+    for a, b in zip(fused_w, plain_w):
+        assert torch.equal(a.detach(), b.detach())
+        assert torch.equal(_shadow(fused_opt, a), _shadow(plain_opt, b))
