@@ -339,10 +339,31 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
   OUT_T* CD = g.c_diag ? reinterpret_cast<OUT_T*>(g.c_diag) + bidx * g.sc : nullptr;
   const bool vec_rows = (g.ldd % 8 == 0) && (g.ldc % 8 == 0) && (g.sc % 8 == 0) &&
                         (g.sd % 8 == 0);
+  // Interior tiles: every thread issues all its 16-byte loads of D at once (one
+  // memory latency per tile instead of one per chunk), before the pipeline's
+  // LDS is released.
+  constexpr int DQ = BM * BN / 8 / NT;
+  static_assert(DQ * NT * 8 == BM * BN, "D chunks must divide evenly over the threads");
+  const bool d_whole = D && vec_rows && m0 + BM <= g.m_lim && n0 + BN <= g.n_lim;
+  u4 dv[DQ];
+  if (d_whole) {
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      const int q = tid + i * NT, r = q / (BN / 8), c8 = (q % (BN / 8)) * 8;
+      dv[i] = *reinterpret_cast<const u4*>(D + (int64_t)(m0 + r) * g.ldd + n0 + c8);
+    }
+  }
   // Every wave is done with the pipeline's LDS before the tile overwrites it.
   __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0) lgkmcnt(0)
   __syncthreads();
-  if (D) {
+  if (d_whole) {
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      const int q = tid + i * NT, r = q / (BN / 8), c8 = (q % (BN / 8)) * 8;
+      *reinterpret_cast<u4*>(reinterpret_cast<T*>(tile) + r * ELD + c8) = dv[i];
+    }
+    __syncthreads();
+  } else if (D) {
     for (int q = tid; q < BM * BN / 8; q += NT) {
       const int r = q / (BN / 8), c8 = (q % (BN / 8)) * 8;
       const int gr = m0 + r, gc = n0 + c8;
@@ -356,19 +377,39 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
     }
     __syncthreads();
   }
+  // Each lane replaces its fragment elements of D with the result; a fragment's
+  // 16 reads of D are issued before its 16 writes (one LDS wait per fragment).
+  if (D) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int col = wcol0 + j * 32 + lrow;
+      for (int j = 0; j < FN; ++j) {
+        const int col = wcol0 + j * 32 + lrow;
+        float dval[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-        float x = g.alpha * acc[i][j][e];
-        if (D) x += g.beta * (float)reinterpret_cast<const T*>(tile)[row * ELD + col];
-        tile[row * ELD + col] = round_out<OUT_T, MODE>(x);
+        for (int e = 0; e < 16; ++e) {
+          const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+          dval[e] = (float)reinterpret_cast<const T*>(tile)[row * ELD + col];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+          tile[row * ELD + col] = round_out<OUT_T, MODE>(g.alpha * acc[i][j][e] + g.beta * dval[e]);
+        }
       }
-    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = wcol0 + j * 32 + lrow;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+          tile[row * ELD + col] = round_out<OUT_T, MODE>(g.alpha * acc[i][j][e]);
+        }
+      }
+  }
   __syncthreads();
   // Straight stores: rows of the tile (on a diagonal tile, columns >= row).
   if (C || CD) {
