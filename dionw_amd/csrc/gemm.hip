@@ -411,14 +411,39 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
       }
   }
   __syncthreads();
-  // Straight stores: rows of the tile (on a diagonal tile, columns >= row).
+  // A diagonal tile of a symmetric product takes its lower triangle from its
+  // upper one inside LDS (reads stay above the diagonal, writes below it), then
+  // leaves whole through the straight stores: its mirror is itself.
+  if (diag_tile) {
+    // Consecutive lanes take consecutive rows r of one chunk column: the gathers
+    // (column r of rows c8 .. c8 + 7) read adjacent elements and the 16-byte
+    // writes fall 4 banks apart.
+    for (int q = tid; q < BM * BN / 8; q += NT) {
+      const int r = q % BM, c8 = (q / BM) * 8;
+      if (c8 >= r) continue;  // no element of this chunk lies below the diagonal
+      OUT_T v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        v[e] = c8 + e < r ? tile[(c8 + e) * ELD + r] : (OUT_T)0.f;
+      OUT_T* dst = tile + r * ELD + c8;
+      if (c8 + 8 <= r) {
+        u4 w;
+        __builtin_memcpy(&w, v, 16);
+        *reinterpret_cast<u4*>(dst) = w;
+      } else {
+        for (int e = 0; e < r - c8; ++e) dst[e] = v[e];
+      }
+    }
+    __syncthreads();
+  }
+  // Straight stores: rows of the tile.
   if (C || CD) {
     for (int q = tid; q < BM * BN / 8; q += NT) {
       const int r = q / (BN / 8), c8 = (q % (BN / 8)) * 8;
       const int gr = m0 + r, gc = n0 + c8;
       if (gr >= g.m_lim || gc >= g.n_lim) continue;
       const OUT_T* src = tile + r * ELD + c8;
-      const bool whole = gc + 8 <= g.n_lim && !(diag_tile && c8 < r) && vec_rows;
+      const bool whole = gc + 8 <= g.n_lim && vec_rows;
       if (whole && !(CD && gr >= gc && gr < gc + 8)) {
         const u4 v = *reinterpret_cast<const u4*>(src);
         if (C) *reinterpret_cast<u4*>(C + (int64_t)gr * g.ldc + gc) = v;
@@ -426,16 +451,17 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
       } else {
         for (int e = 0; e < 8; ++e) {
           const int c = gc + e;
-          if (c >= g.n_lim || (diag_tile && c8 + e < r)) continue;
+          if (c >= g.n_lim) continue;
           if (C) C[(int64_t)gr * g.ldc + c] = src[e];
           if (CD) CD[(int64_t)gr * g.ldc + c] = (OUT_T)((float)src[e] + (gr == c ? g.diag_shift : 0.f));
         }
       }
     }
   }
-  // Transposed / mirrored stores: column c of the tile becomes row n0 + c.
-  // Lane -> (8 columns, 8 row blocks of 8) so that 8 lanes write 128 contiguous bytes.
-  OUT_T* TT = CT ? CT : nullptr;
+  // Transposed / mirrored stores: column c of the tile becomes row n0 + c (off-diagonal
+  // tiles only). Lane -> (8 columns, 8 row blocks of 8) so that 8 lanes write 128
+  // contiguous bytes.
+  OUT_T* TT = CT && !diag_tile ? CT : nullptr;
   if (TT) {
     const int64_t ldt = g.ct ? g.ldct : g.ldc;
     for (int q = tid; q < BM * BN / 8; q += NT) {
@@ -447,22 +473,16 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
       OUT_T v[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = tile[(r8 + e) * ELD + c];
-      const bool mirror_skip_any = diag_tile && r8 + 7 >= c;
-      if (!mirror_skip_any && gr + 8 <= g.m_lim && ldt % 8 == 0 && g.sct % 8 == 0 &&
+      if (gr + 8 <= g.m_lim && ldt % 8 == 0 && g.sct % 8 == 0 &&
           (reinterpret_cast<uintptr_t>(TT) & 15) == 0) {
         u4 w;
         __builtin_memcpy(&w, v, 16);
         *reinterpret_cast<u4*>(TT + (int64_t)gc * ldt + gr) = w;
-        if (g.sym && CD) {
-          OUT_T vd[8];
-          for (int e = 0; e < 8; ++e) vd[e] = v[e];  // off-diagonal: no shift
-          __builtin_memcpy(&w, vd, 16);
-          *reinterpret_cast<u4*>(CD + (int64_t)gc * g.ldc + gr) = w;
-        }
+        if (g.sym && CD) *reinterpret_cast<u4*>(CD + (int64_t)gc * g.ldc + gr) = w;  // no shift
       } else {
         for (int e = 0; e < 8; ++e) {
           const int r = r8 + e;
-          if (m0 + r >= g.m_lim || (diag_tile && r >= c)) continue;
+          if (m0 + r >= g.m_lim) continue;
           TT[(int64_t)gc * ldt + m0 + r] = v[e];
           if (g.sym && CD) CD[(int64_t)gc * g.ldc + m0 + r] = v[e];
         }
