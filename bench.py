@@ -439,7 +439,9 @@ def main() -> int:
             "peak": PEAK_MFMA_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(ns_tflops / PEAK_MFMA_TFLOPS, 4),
-            "traffic": traffic_bytes(),
+            # Measured for the Llama-3-8B gate/up product only; other workloads'
+            # dominant launches have other shapes.
+            "traffic": traffic_bytes() if args.config == "llama3-8b" else None,
             "avg_launch_us": round(ns["ms"] * 1e3 / max(ns.get("launches", 0), 1), 1),
             "launches_per_step": ns.get("launches", 0) // div,
         },
