@@ -95,6 +95,19 @@ class Timeline:
                 entry["flops"] += batch * ns_flops(kind, r_real, c_real)
                 # MFMA product launches of the call: 18 for the Gram iteration, 15 otherwise.
                 entry["launches"] = entry.get("launches", 0) + (18 if kind == 0 and c_real > r_real else 15)
+            elif name == "dionw_newton_schulz_group":
+                # Reported with the single calls: the same products, grouped.
+                del out[name]
+                entry = out["dionw_newton_schulz"]
+                entry["ms"] += start.elapsed_time(end)
+                entry["calls"] += 1
+                n = a[0]
+                for i in range(n):
+                    entry["flops"] += a[2][i] * ns_flops(a[1][i], a[7][i], a[8][i])
+                # The library's own count of the products it launched for the call.
+                launches = self._restore[0].library().dionw_newton_schulz_group_launches(
+                    n, a[1], a[2], a[3], a[4], a[7], a[8])
+                entry["launches"] = entry.get("launches", 0) + launches
             elif name == "dionw_accumulate_scores":
                 count, rows, cols = a[1], a[2], a[3]
                 entry["bytes"] += 12.0 * count * rows * cols

@@ -43,6 +43,8 @@ _f32 = ctypes.c_float
 _f64 = ctypes.c_double
 _pp = ctypes.POINTER(ctypes.c_void_p)
 _pi64 = ctypes.POINTER(ctypes.c_int64)
+_pi32 = ctypes.POINTER(ctypes.c_int32)
+_psize = ctypes.POINTER(ctypes.c_size_t)
 
 # name -> (restype, argtypes); mirrors include/dionw_hip.h.
 SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
@@ -70,6 +72,14 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [_i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _i32, _i64, _i64, _p,
          ctypes.c_size_t, _p],
+    ),
+    "dionw_newton_schulz_group": (
+        ctypes.c_int,
+        [_i32, _pi32, _pi64, _pi64, _pi64, _pp, _pp, _pi64, _pi64, _pp, _pi32, _pi64, _pi64,
+         _pp, _psize, _p],
+    ),
+    "dionw_newton_schulz_group_launches": (
+        ctypes.c_int64, [_i32, _pi32, _pi64, _pi64, _pi64, _pi64, _pi64],
     ),
     "dionw_normuon_stats": (
         ctypes.c_int,

@@ -14,15 +14,20 @@ On the HIP path this is five to seven launches per run, each over the whole
 run through pointer tables: accumulate/sumsq, select, prepare (decay + the
 normalized 16-bit input in both orientations), the Newton-Schulz products,
 NorMuon statistics and the fused apply (which also takes a due GPU EMA lerp of
-the run's weights). A user-supplied orthogonalization
-(``newton_schulz_fn`` replaced) receives the float32 input rows instead, as
-the reference's plugin does.
+the run's weights). Within ``Dion.step`` the runs queue after the prepare
+pass and the step's Newton-Schulz calls run together in grouped launches
+(``RunQueue``); the runs are independent, so each run's results are the same.
+A user-supplied orthogonalization (``newton_schulz_fn`` replaced) receives the
+float32 input rows instead, as the reference's plugin does.
 """
 
 from __future__ import annotations
 
 import math
+from collections.abc import Callable
+from contextvars import ContextVar
 from dataclasses import dataclass
+from functools import partial
 from typing import Any, Final
 
 import torch
@@ -39,9 +44,17 @@ from dionw_amd._keys import (
 )
 from dionw_amd.ema._fusion import ACTIVE_EMA
 from dionw_amd.matrix_update import MomentumForm, RowNormalization
-from dionw_amd.newton_schulz import HipOrthogonalize, run_newton_schulz
+from dionw_amd.newton_schulz import (
+    HipOrthogonalize,
+    NewtonSchulzCall,
+    group_launches,
+    newton_schulz_call,
+    run_newton_schulz,
+    run_newton_schulz_call,
+    run_newton_schulz_group,
+)
 
-__all__ = ["MAX_RUN_ELEMENTS", "run_elements", "step_run"]
+__all__ = ["ACTIVE_RUNS", "MAX_RUN_ELEMENTS", "RunQueue", "run_elements", "step_run"]
 
 # AdamW update RMS that matrix steps match (Moonshot's 0.2).
 ADAMW_UPDATE_RMS: Final[float] = 0.2
@@ -114,10 +127,76 @@ def _round8(n: int) -> int:
     return (n + 7) // 8 * 8
 
 
+# Dion.step sets this around its bucket loop: step_run then queues each fused
+# run after its momentum passes, and the queue finishes the queued runs
+# together, with one grouped Newton-Schulz call (small runs fill the CUs that
+# a large run's products leave idle; each run's results are unchanged).
+ACTIVE_RUNS: ContextVar[RunQueue | None] = ContextVar("dionw_amd_active_runs", default=None)
+
+# A queue holds at most this many runs (the library groups up to 8 at a time)
+# and this many bytes of Newton-Schulz buffers: queued runs each keep their own.
+QUEUE_RUNS: Final[int] = 8
+QUEUE_BYTES: Final[int] = 32 * 2**30
+
+
+class RunQueue:
+    """Bucket runs waiting for their Newton-Schulz call and the passes after it."""
+
+    def __init__(self) -> None:
+        self._calls: list[NewtonSchulzCall] = []
+        self._finish: list[Callable[[], None]] = []
+        self._bytes = 0
+        self._stream: int | None = None
+
+    def slot(self, nbytes: int, stream: int) -> str:
+        """Name suffix of the next run's buffers; flushes first if that run does not fit."""
+        if self._calls and (len(self._calls) >= QUEUE_RUNS or stream != self._stream
+                            or self._bytes + nbytes > QUEUE_BYTES):
+            self.flush()
+        return f"#{len(self._calls)}"
+
+    def add(self, call: NewtonSchulzCall, finish: Callable[[], None], nbytes: int,
+            stream: int) -> None:
+        self._calls.append(call)
+        self._finish.append(finish)
+        self._bytes += nbytes
+        self._stream = stream
+
+    def flush(self) -> None:
+        """Run the queued Newton-Schulz calls and finish the runs, in queue order.
+
+        When grouping saves no launch, each run's iteration is followed by its
+        own passes instead, which then find its output still in cache.
+        """
+        if not self._calls:
+            return
+        calls, finish, stream = self._calls, self._finish, self._stream
+        self._calls, self._finish, self._bytes, self._stream = [], [], 0, None
+        if len(calls) > 1 and group_launches(calls) < sum(group_launches([c]) for c in calls):
+            run_newton_schulz_group(calls, stream)
+            for done in finish:
+                done()
+            return
+        for call, done in zip(calls, finish):
+            run_newton_schulz_call(call, stream)
+            done()
+
+
+def _ns_bytes(ortho: HipOrthogonalize, blocks: int, k: int, cols: int) -> int:
+    """Bytes of a fused run's Newton-Schulz buffers (inputs, output, workspace)."""
+    p_pad, j_pad = _round8(k), _round8(cols)
+    r, c = min(p_pad, j_pad), max(p_pad, j_pad)
+    work = int(_lib.library().dionw_newton_schulz_workspace(ortho.lib_kind, blocks, r, c))
+    return 2 * 2 * blocks * p_pad * j_pad + 2 * blocks * k * cols + work
+
+
 def step_run(
     bucket: Bucket, positions: list[int] | range, group: dict[str, Any], state: ParamState
 ) -> None:
     """Apply one Dion step to the consecutive bucket parameters ``positions``.
+
+    Inside ``Dion.step`` a fused run is queued after its momentum passes and
+    finished when the step's queue is flushed.
 
     Raises:
         RuntimeError: If a parameter has no gradient.
@@ -138,6 +217,10 @@ def step_run(
     safety = ortho.norm_safety if fused else 1.0
     grads = _lib.ptr_array(run.grads)
     momentum = run.momentum
+    queue = ACTIVE_RUNS.get() if fused else None
+    nbytes = _ns_bytes(ortho, blocks, k, cols) if queue is not None else 0
+    # Buffers still in use when a queued run finishes get names of their own.
+    own = queue.slot(nbytes, stream) if queue is not None else ""
 
     den = _workspace.buffer(device, "den", (blocks,), torch.float32)
     rowsq = _workspace.buffer(device, "rowsq", (blocks * rows,), torch.float32)
@@ -145,8 +228,8 @@ def step_run(
     idx = slot = None
     if selected:
         scores = _workspace.buffer(device, "scores", (blocks * rows,), torch.float32)
-        idx = _workspace.buffer(device, "idx", (blocks, k), torch.int32)
-        slot = _workspace.buffer(device, "slot", (blocks, rows), torch.int32)
+        idx = _workspace.buffer(device, "idx" + own, (blocks, k), torch.int32)
+        slot = _workspace.buffer(device, "slot" + own, (blocks, rows), torch.int32)
         _lib.call("dionw_accumulate_scores", grads, count, per_param * rows, cols,
                   momentum.data_ptr(), scores.data_ptr(), rowsq.data_ptr(), stream)
         _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k,
@@ -161,12 +244,18 @@ def step_run(
 
     if fused:
         p_pad, j_pad = _round8(k), _round8(cols)
-        xr = _workspace.buffer(device, "ns_xr", (blocks, p_pad, j_pad), ortho.dtype)
-        xt = _workspace.buffer(device, "ns_xt", (blocks, j_pad, p_pad), ortho.dtype)
+        xr = _workspace.buffer(device, "ns_xr" + own, (blocks, p_pad, j_pad), ortho.dtype)
+        xt = _workspace.buffer(device, "ns_xt" + own, (blocks, j_pad, p_pad), ortho.dtype)
         _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
                   den.data_ptr(), blocks, rows, cols, k, p_pad, j_pad, mu, int(nesterov), 1,
                   ortho.elem, xr.data_ptr(), xt.data_ptr(), stream)
-        orthogonal = _workspace.buffer(device, "ns_out", (blocks, k, cols), torch.bfloat16)
+        orthogonal = _workspace.buffer(device, "ns_out" + own, (blocks, k, cols), torch.bfloat16)
+        if queue is not None:
+            call = newton_schulz_call(ortho, blocks, k, cols, xr, xt, orthogonal,
+                                      "ns_workspace" + own)
+            queue.add(call, partial(_finish_run, run, bucket, positions, group, orthogonal, idx,
+                                    slot, step, stream), nbytes, stream)
+            return
         run_newton_schulz(ortho, blocks, k, cols, xr, xt, orthogonal, stream)
     else:
         raw = torch.empty(blocks, k, cols, device=device, dtype=torch.float32)
@@ -175,7 +264,28 @@ def step_run(
                   _lib.F32, raw.data_ptr(), None, stream)
         orthogonal = ortho(raw, NEWTON_SCHULZ_EPS)
         orthogonal = orthogonal.to(torch.bfloat16).contiguous()
+    _finish_run(run, bucket, positions, group, orthogonal, idx, slot, step, stream)
 
+
+def _finish_run(
+    run: _Run,
+    bucket: Bucket,
+    positions: list[int] | range,
+    group: dict[str, Any],
+    orthogonal: Tensor,
+    idx: Tensor | None,
+    slot: Tensor | None,
+    step: float,
+    stream: int,
+) -> None:
+    """NorMuon statistics and the weight update of a run whose orthogonalized
+    rows ``orthogonal`` ([blocks, k, cols] bf16) are ready (_matrix_step.py:274-311)."""
+    device = run.momentum.device
+    blocks, rows, cols, k = run.blocks, bucket.rows, bucket.cols, bucket.selected_rows
+    count = len(run.params)
+    per_param = bucket.blocks_per_param
+    lr = float(group["lr"])
+    idx_ptr = None if idx is None else idx.data_ptr()
     rowd = scale = None
     match RowNormalization(group[ROW_NORMALIZATION_KEY]):
         case RowNormalization.NORMUON:

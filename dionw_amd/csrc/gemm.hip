@@ -23,6 +23,8 @@
 
 #include <cmath>
 #include <mutex>
+#include <vector>
+#include <algorithm>
 
 namespace dionw {
 namespace {
@@ -497,8 +499,9 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
+// One output tile: logical tile w of the problem (batch index w / tiles).
 template <typename T, typename OUT_T, int MODE, typename CFG>
-__global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs g, int batch) {
+__device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
   constexpr int PBM = CFG::BM, PBN = CFG::BN, PWN = CFG::WN, PSTAGES = CFG::STAGES;
   constexpr int PSTAGE_ELEMS = CFG::stage_elems, LA = CFG::loads_a, LB = CFG::loads_b;
   constexpr int SBK = CFG::BK, CPR = SBK / 8;  // stage depth, 16-byte chunks per row
@@ -511,15 +514,7 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / PWN, wn = wave % PWN;
 
-  // XCD-aware order: the hardware deals workgroup w to XCD w % 8; give each
-  // XCD a contiguous range of logical tiles so that its L2 sees reuse.
   const int tiles = g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
-  const int total = tiles * batch;
-  int w = blockIdx.x;
-  {
-    const int per = total / 8, extra = total % 8, x = w % 8, i = w / 8;
-    w = x * per + min(x, extra) + i;
-  }
   const int64_t bidx = w / tiles;
   const int t = w - (int)bidx * tiles;
   int tm, tn;
@@ -619,6 +614,47 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs 
       g, acc, bidx, m0, n0, wm * WTM, wn * WTN, g.sym && tm == tn, smem);
 }
 
+// XCD-aware order: the hardware deals workgroup b to XCD b % 8; each XCD gets a
+// contiguous range of the problem's logical tiles, so that its L2 sees reuse.
+// Returns -1 for the b that only pad the grid to a multiple of 8.
+__device__ __forceinline__ int xcd_tile(int b, int total) {
+  const int per = total / 8, extra = total % 8, x = b % 8, i = b / 8;
+  if (i >= per + (x < extra ? 1 : 0)) return -1;
+  return x * per + min(x, extra) + i;
+}
+
+__device__ __forceinline__ int tile_count(const GemmArgs& g) {
+  return g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
+}
+
+template <typename T, typename OUT_T, int MODE, typename CFG>
+__global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs g, int batch) {
+  pipe_tile<T, OUT_T, MODE, CFG>(g, xcd_tile((int)blockIdx.x, tile_count(g) * batch));
+}
+
+// Several independent products in one launch (the same product of several
+// Newton-Schulz runs): problem q owns workgroups [start[q], start[q + 1]), each
+// range a multiple of 8 long so that every problem keeps its XCD-aware order.
+constexpr int kMaxGroup = 8;
+
+struct GemmGroup {
+  GemmArgs g[kMaxGroup];
+  int batch[kMaxGroup];
+  int start[kMaxGroup];
+  int count;
+};
+
+template <typename T, typename OUT_T, int MODE, typename CFG>
+__global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_group_kernel(GemmGroup grp) {
+  int q = 0;
+  for (int j = 1; j < grp.count; ++j)
+    if ((int)blockIdx.x >= grp.start[j]) q = j;
+  const GemmArgs& g = grp.g[q];
+  const int w = xcd_tile((int)blockIdx.x - grp.start[q], tile_count(g) * grp.batch[q]);
+  if (w < 0) return;  // the whole workgroup: w depends on blockIdx only
+  pipe_tile<T, OUT_T, MODE, CFG>(g, w);
+}
+
 // ---- launch configuration ----------------------------------------------------
 
 
@@ -661,49 +697,110 @@ int launch_cfg(const Problem& p, hipStream_t stream) {
   return check_launch("gemm_nt");
 }
 
-template <typename T, typename OUT_T, int MODE, typename CFG>
-int launch_pipe(const Problem& p, hipStream_t stream) {
-  GemmArgs g = p.g;
+template <typename CFG>
+constexpr size_t pipe_lds_bytes() {
+  return CFG::lds_bytes > epi_lds_bytes<CFG::BM, CFG::BN>() ? CFG::lds_bytes
+                                                            : epi_lds_bytes<CFG::BM, CFG::BN>();
+}
+
+// The kernel-side fields of a pipelined product; returns its workgroup count
+// (tiles x batch) or -1 with the error set.
+template <typename CFG>
+int64_t pipe_args(const Problem& p, GemmArgs& g) {
+  g = p.g;
   g.ct_vec = !g.ct || (g.ldct % 4 == 0 && g.sct % 4 == 0 &&
                        (reinterpret_cast<uintptr_t>(g.ct) & 7) == 0);
   if (g.c_diag && g.sym) g.ct_vec = g.ct_vec && g.ldc % 4 == 0 && g.sc % 4 == 0;
-  constexpr size_t lds_bytes = CFG::lds_bytes > epi_lds_bytes<CFG::BM, CFG::BN>()
-                                  ? CFG::lds_bytes : epi_lds_bytes<CFG::BM, CFG::BN>();
-  auto kern = gemm_nt_pipe_kernel<T, OUT_T, MODE, CFG>;
-  static std::once_flag once;
-  static hipError_t attr_rc = hipSuccess;
-  std::call_once(once, [&] {
-    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-  });
-  if (attr_rc != hipSuccess) {
-    set_error("gemm: hipFuncSetAttribute failed: %s", hipGetErrorString(attr_rc));
-    return kHipError;
-  }
   g.tiles_m = (g.m + CFG::BM - 1) / CFG::BM;
   g.tiles_n = (g.n + CFG::BN - 1) / CFG::BN;
   if (g.sym && (g.m != g.n || CFG::BM != CFG::BN)) {
     set_error("gemm: symmetric mode needs a square output and square tiles");
-    return kInvalid;
+    return -1;
   }
   const int64_t tiles = g.sym ? (int64_t)g.tiles_m * (g.tiles_m + 1) / 2
                               : (int64_t)g.tiles_m * g.tiles_n;
   if (tiles * p.batch > INT32_MAX) {
     set_error("gemm: grid too large");
-    return kInvalid;
+    return -1;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * p.batch)), dim3(CFG::threads), lds_bytes, stream,
-                     g, (int)p.batch);
+  return tiles * p.batch;
+}
+
+// Raises a kernel's dynamic LDS limit once per process (one flag per kernel).
+template <auto kern>
+int allow_lds(size_t lds_bytes) {
+  static std::once_flag once;
+  static hipError_t rc = hipSuccess;
+  std::call_once(once, [&] {
+    rc = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+  });
+  if (rc != hipSuccess) {
+    set_error("gemm: hipFuncSetAttribute failed: %s", hipGetErrorString(rc));
+    return kHipError;
+  }
+  return kOk;
+}
+
+template <typename T, typename OUT_T, int MODE, typename CFG>
+int launch_pipe(const Problem& p, hipStream_t stream) {
+  constexpr size_t lds_bytes = pipe_lds_bytes<CFG>();
+  constexpr auto kern = gemm_nt_pipe_kernel<T, OUT_T, MODE, CFG>;
+  DIONW_TRY(allow_lds<kern>(lds_bytes));
+  GemmArgs g;
+  const int64_t wgs = pipe_args<CFG>(p, g);
+  if (wgs < 0) return kInvalid;
+  hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(CFG::threads), lds_bytes, stream, g,
+                     (int)p.batch);
   return check_launch("gemm_nt_pipe");
 }
 
+// One launch of up to kMaxGroup products on 256x256 tiles with 64-deep stages,
+// longest k first (its tiles take longest, so they start first).
+template <typename T, typename OUT_T, int MODE>
+int launch_pipe_group(const std::vector<const Problem*>& ps, hipStream_t stream) {
+  using Big64 = PipeCfg<256, 256, 4, 4, 2, 64>;
+  constexpr size_t lds_bytes = pipe_lds_bytes<Big64>();
+  constexpr auto kern = gemm_nt_pipe_group_kernel<T, OUT_T, MODE, Big64>;
+  DIONW_TRY(allow_lds<kern>(lds_bytes));
+  std::vector<const Problem*> order(ps);
+  std::stable_sort(order.begin(), order.end(),
+                   [](const Problem* a, const Problem* b) { return a->g.k > b->g.k; });
+  GemmGroup grp{};
+  grp.count = (int)order.size();
+  int64_t start = 0;
+  for (int q = 0; q < grp.count; ++q) {
+    const int64_t wgs = pipe_args<Big64>(*order[q], grp.g[q]);
+    if (wgs < 0) return kInvalid;
+    grp.batch[q] = (int)order[q]->batch;
+    grp.start[q] = (int)start;
+    start += (wgs + 7) / 8 * 8;
+    if (start > INT32_MAX) {
+      set_error("gemm: grid too large");
+      return kInvalid;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)start), dim3(Big64::threads), lds_bytes, stream, grp);
+  return check_launch("gemm_nt_pipe_group");
+}
+
+// Workgroups a tile size yields (symmetric products: upper-triangle tiles).
+int64_t wgs_of(const Problem& p, int tile) {
+  const int64_t tm = (p.g.m + tile - 1) / tile, tn = (p.g.n + tile - 1) / tile;
+  return p.batch * (p.g.sym ? tm * (tm + 1) / 2 : tm * tn);
+}
+
+// Rounds of workgroups over the 256 CUs (one 256x256 or two 128x128 per CU),
+// in units of one 256x256 round: a 128x128 round counts 2 * 128^2 / 256^2 *
+// 1.2 (the smaller tile's measured rate on the large shapes is 1/1.2 of the
+// 256x256 tile's).
+// Both in tenths of a 256x256 round (a 128x128 round is exactly 0.6).
+int64_t big_tenths(const Problem& p) { return 10 * ((wgs_of(p, 256) + 255) / 256); }
+int64_t mid_tenths(const Problem& p) { return 6 * ((wgs_of(p, 128) + 511) / 512); }
+
 template <typename T, typename OUT_T, int MODE>
 int launch_typed(const Problem& p, hipStream_t stream) {
-  // Workgroups a tile size yields (symmetric products: upper-triangle tiles).
-  auto wgs = [&](int tile) {
-    const int64_t tm = (p.g.m + tile - 1) / tile, tn = (p.g.n + tile - 1) / tile;
-    return p.batch * (p.g.sym ? tm * (tm + 1) / 2 : tm * tn);
-  };
+  auto wgs = [&](int tile) { return wgs_of(p, tile); };
   // 256x256 tiles run 16 waves of 64x64, 128x128 tiles 4 waves of 64x64. A k
   // depth that is a multiple of 64 takes 64-deep stages in a two-stage ring (half
   // the barriers per MFMA of 32-deep stages); other multiples of 32, four
@@ -727,13 +824,8 @@ int launch_typed(const Problem& p, hipStream_t stream) {
   if (DIONW_FORCE_KERNEL == 4) return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
 #endif
   if (k32) {
-    // Rounds of workgroups over the 256 CUs (one 256x256 or two 128x128 per CU)
-    // times the work of one round, the 128x128 rounds weighted 1.2 (its measured
-    // rate on the large shapes is 1/1.2 of the 256x256 tile's): the smaller tile
-    // wins when the big one leaves CUs idle or pads a ragged side.
-    const double big = (double)((wgs(256) + 255) / 256) * (256.0 * 256.0);
-    const double mid = (double)((wgs(128) + 511) / 512) * (2.0 * 128.0 * 128.0) * 1.2;
-    if (big <= mid) {
+    // The smaller tile wins when the big one leaves CUs idle or pads a ragged side.
+    if (big_tenths(p) <= mid_tenths(p)) {
       if (k64) return launch_pipe<T, OUT_T, MODE, Big64>(p, stream);
       return launch_pipe<T, OUT_T, MODE, Big32>(p, stream);
     }
@@ -744,11 +836,15 @@ int launch_typed(const Problem& p, hipStream_t stream) {
   return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
 }
 
+bool operands_ok(const GemmArgs& g) {
+  return !(g.k % 8 || g.lda % 8 || g.ldb % 8 || g.sa % 8 || g.sb % 8 || !aligned16(g.a) ||
+           !aligned16(g.b));
+}
+
 int launch(const Problem& p, hipStream_t stream) {
   const GemmArgs& g = p.g;
   if (g.m <= 0 || g.n <= 0 || g.k <= 0 || p.batch <= 0) return kOk;
-  if (g.k % 8 || g.lda % 8 || g.ldb % 8 || g.sa % 8 || g.sb % 8 ||
-      !aligned16(g.a) || !aligned16(g.b)) {
+  if (!operands_ok(g)) {
     set_error("gemm: k, operand row strides and batch strides must be multiples of 8 "
               "elements and operands 16-byte aligned");
     return kInvalid;
@@ -760,6 +856,56 @@ int launch(const Problem& p, hipStream_t stream) {
   if (p.elem == kBF16) return launch_typed<__bf16, __bf16, kOutSame>(p, stream);
   set_error("gemm: unsupported element type %d", p.elem);
   return kInvalid;
+}
+
+// Whether one grouped launch beats one launch per product. Time in 256x256
+// rounds times k: each product alone takes its better tile (the launcher's
+// rule); grouped, the 256x256 tiles of all of them fill the CUs longest first,
+// which costs their total work over the 256 CUs plus about half a round of the
+// shortest tiles, and no less than the longest tile.
+bool group_pays(const std::vector<const Problem*>& ps) {
+  double separate = 0.0, work = 0.0, kmax = 0.0, kmin = 1e300;
+  for (const Problem* p : ps) {
+    const double k = (double)p->g.k;
+    separate += k * 0.1 * (double)std::min(big_tenths(*p), mid_tenths(*p));
+    work += k * (double)wgs_of(*p, 256) / 256.0;
+    kmax = std::max(kmax, k);
+    kmin = std::min(kmin, k);
+  }
+  return std::max(work + 0.5 * kmin, kmax) < separate;
+}
+
+// Independent products in as few launches as possible: one grouped launch when
+// every product has the same types and a k depth that is a multiple of 64 (the
+// 256x256 tile with 64-deep stages serves them all) and grouping pays, else one
+// launch each.
+std::vector<const Problem*> live_products(const std::vector<const Problem*>& ps) {
+  std::vector<const Problem*> live;
+  for (const Problem* p : ps)
+    if (p->g.m > 0 && p->g.n > 0 && p->g.k > 0 && p->batch > 0) live.push_back(p);
+  return live;
+}
+
+bool groups(const std::vector<const Problem*>& live) {
+  bool together = live.size() >= 2 && live.size() <= (size_t)kMaxGroup;
+  for (const Problem* p : live)
+    together = together && p->elem == live[0]->elem && p->out_mode == live[0]->out_mode &&
+               p->g.k % 64 == 0 && p->batch <= INT32_MAX && operands_ok(p->g);
+  return together && group_pays(live);
+}
+
+int launch_group(const std::vector<const Problem*>& ps, hipStream_t stream) {
+  const std::vector<const Problem*> live = live_products(ps);
+  if (!groups(live)) {
+    for (const Problem* p : live) DIONW_TRY(launch(*p, stream));
+    return kOk;
+  }
+  if (live[0]->elem == kF16) {
+    if (live[0]->out_mode == kOutBf16ViaF16)
+      return launch_pipe_group<_Float16, __bf16, kOutBf16ViaF16>(live, stream);
+    return launch_pipe_group<_Float16, _Float16, kOutSame>(live, stream);
+  }
+  return launch_pipe_group<__bf16, __bf16, kOutSame>(live, stream);
 }
 
 // ---- Newton-Schulz drivers ---------------------------------------------------
@@ -900,10 +1046,16 @@ size_t dionw_newton_schulz_workspace(int32_t kind, int64_t batch, int64_t r, int
   return elems_needed(kind, batch, r, c) * 2;
 }
 
-int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void* xt,
-                        int64_t r_real, int64_t c_real, void* out, int32_t out_transposed,
-                        int64_t out_ld, int64_t out_stride, void* workspace,
-                        size_t workspace_bytes, hipStream_t stream) {
+}  // extern "C"
+
+namespace dionw {
+namespace {
+
+// The products of one Newton-Schulz call, in order (validated; nothing launched).
+int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void* xt,
+               int64_t r_real, int64_t c_real, void* out, int32_t out_transposed, int64_t out_ld,
+               int64_t out_stride, void* workspace, size_t workspace_bytes,
+               std::vector<Problem>& prog) {
   DIONW_REQUIRE(kind == kGram || kind == kPolarExpress || kind == kKeller,
                 "newton_schulz: unknown kind %d", kind);
   DIONW_REQUIRE(x && xt && out && workspace, "newton_schulz: null pointer");
@@ -932,7 +1084,7 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
     Problem p = product(elem, batch, R, R, C, X, X);
     set_out(p, G);
     make_symmetric(p);
-    DIONW_TRY(launch(p, stream));
+    prog.push_back(p);
     Mat xt_cur = XT;
     for (int i = 0; i < 5; ++i) {
       const float a = (float)coef[i][0], bb = (float)coef[i][1], cc = (float)coef[i][2];
@@ -941,12 +1093,12 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
         p = product(elem, batch, R, C, R, Q, xt_cur);
         set_out(p, X);
         set_out_t(p, XT2);
-        DIONW_TRY(launch(p, stream));
+        prog.push_back(p);
         xt_cur = XT2;
         p = product(elem, batch, R, R, C, X, X);
         set_out(p, G);
         make_symmetric(p);
-        DIONW_TRY(launch(p, stream));
+        prog.push_back(p);
       }
       // Z = c G G + b G; at iterations 0 and 2 also Q = Z + a I.
       p = product(elem, batch, R, R, R, G, G);
@@ -957,14 +1109,14 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
         p.g.c_diag = Q.p;
         p.g.diag_shift = a;
       }
-      DIONW_TRY(launch(p, stream));
+      prog.push_back(p);
       if (i != 0 && i != 2) {
         // Q = a Q + Q Z
         p = product(elem, batch, R, R, R, Q, Z);
         set_addend(p, Q, 1.f, a);
         set_out(p, Q2);
         make_symmetric(p);
-        DIONW_TRY(launch(p, stream));
+        prog.push_back(p);
         std::swap(Q, Q2);
       }
       if (i < 4 && i + 1 != 2) {
@@ -973,12 +1125,12 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
         set_addend(p, G, 1.f, a);
         set_out(p, RZ);
         make_symmetric(p);
-        DIONW_TRY(launch(p, stream));
+        prog.push_back(p);
         p = product(elem, batch, R, R, R, Z, RZ);
         set_addend(p, RZ, 1.f, a);
         set_out(p, G2);
         make_symmetric(p);
-        DIONW_TRY(launch(p, stream));
+        prog.push_back(p);
         std::swap(G, G2);
       }
     }
@@ -986,7 +1138,8 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
     p = product(elem, batch, R, C, R, Q, xt_cur);
     p.out_mode = kOutBf16ViaF16;
     set_final_out(p, out, out_transposed, out_ld, out_stride, r_real, c_real);
-    return launch(p, stream);
+    prog.push_back(p);
+    return kOk;
   }
 
   // Standard iteration (square Gram blocks, fp16) or the bf16 quintic:
@@ -1002,26 +1155,125 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
     Problem p = product(elem, batch, R, R, C, X, X);
     set_out(p, G);
     make_symmetric(p);
-    DIONW_TRY(launch(p, stream));
+    prog.push_back(p);
     p = product(elem, batch, R, R, R, G, G);
     set_addend(p, G, cc, bb);
     set_out(p, P);
     make_symmetric(p);
-    DIONW_TRY(launch(p, stream));
+    prog.push_back(p);
     p = product(elem, batch, R, C, R, P, xt_cur);
     set_addend(p, X, 1.f, a);
     if (i < 4) {
       set_out(p, X);  // X is only read as the addend, element by element
       set_out_t(p, xt_next);
-      DIONW_TRY(launch(p, stream));
+      prog.push_back(p);
       std::swap(xt_cur, xt_next);
     } else {
       if (kind == kGram) p.out_mode = kOutBf16ViaF16;
       set_final_out(p, out, out_transposed, out_ld, out_stride, r_real, c_real);
-      DIONW_TRY(launch(p, stream));
+      prog.push_back(p);
     }
   }
   return kOk;
+}
+
+bool same_structure(const std::vector<Problem>& a, const std::vector<Problem>& b) {
+  if (a.size() != b.size()) return false;
+  for (size_t i = 0; i < a.size(); ++i)
+    if (a[i].elem != b[i].elem || a[i].out_mode != b[i].out_mode) return false;
+  return true;
+}
+
+// Runs whose sequences match product by product (length and types) go
+// together, kMaxGroup at a time: one launch per position of the sequence when
+// grouping pays. Counts the launches in *launches and, if issue, launches them.
+int walk_groups(const std::vector<std::vector<Problem>>& progs, bool issue, hipStream_t stream,
+                int64_t* launches) {
+  const int count = (int)progs.size();
+  std::vector<char> done(count, 0);
+  for (int i = 0; i < count; ++i) {
+    if (done[i]) continue;
+    std::vector<int> runs{i};
+    done[i] = 1;
+    for (int j = i + 1; j < count && runs.size() < (size_t)kMaxGroup; ++j)
+      if (!done[j] && same_structure(progs[i], progs[j])) {
+        runs.push_back(j);
+        done[j] = 1;
+      }
+    for (size_t pos = 0; pos < progs[i].size(); ++pos) {
+      std::vector<const Problem*> ps;
+      for (int j : runs) ps.push_back(&progs[j][pos]);
+      const std::vector<const Problem*> live = live_products(ps);
+      *launches += groups(live) ? 1 : (int64_t)live.size();
+      if (issue) DIONW_TRY(launch_group(ps, stream));
+    }
+  }
+  return kOk;
+}
+
+}  // namespace
+}  // namespace dionw
+
+extern "C" {
+
+int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void* xt,
+                        int64_t r_real, int64_t c_real, void* out, int32_t out_transposed,
+                        int64_t out_ld, int64_t out_stride, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  std::vector<Problem> prog;
+  DIONW_TRY(ns_program(kind, batch, r, c, x, xt, r_real, c_real, out, out_transposed, out_ld,
+                       out_stride, workspace, workspace_bytes, prog));
+  for (const Problem& p : prog) DIONW_TRY(launch(p, stream));
+  return kOk;
+}
+
+int dionw_newton_schulz_group(int32_t count, const int32_t* kind, const int64_t* batch,
+                              const int64_t* r, const int64_t* c, void* const* x,
+                              void* const* xt, const int64_t* r_real, const int64_t* c_real,
+                              void* const* out, const int32_t* out_transposed,
+                              const int64_t* out_ld, const int64_t* out_stride,
+                              void* const* workspace, const size_t* workspace_bytes,
+                              hipStream_t stream) {
+  DIONW_REQUIRE(count >= 0 && count <= 4096, "newton_schulz_group: bad count %d", count);
+  if (count == 0) return kOk;
+  DIONW_REQUIRE(kind && batch && r && c && x && xt && r_real && c_real && out &&
+                    out_transposed && out_ld && out_stride && workspace && workspace_bytes,
+                "newton_schulz_group: null argument array");
+  // Products of different runs execute together: their workspaces must not overlap.
+  for (int i = 0; i < count; ++i)
+    for (int j = i + 1; j < count; ++j) {
+      const auto* a = static_cast<const char*>(workspace[i]);
+      const auto* b = static_cast<const char*>(workspace[j]);
+      DIONW_REQUIRE(a + workspace_bytes[i] <= b || b + workspace_bytes[j] <= a,
+                    "newton_schulz_group: workspaces of runs %d and %d overlap", i, j);
+    }
+  std::vector<std::vector<Problem>> progs(count);
+  for (int i = 0; i < count; ++i)
+    DIONW_TRY(ns_program(kind[i], batch[i], r[i], c[i], x[i], xt[i], r_real[i], c_real[i],
+                         out[i], out_transposed[i], out_ld[i], out_stride[i], workspace[i],
+                         workspace_bytes[i], progs[i]));
+  int64_t launches = 0;
+  return walk_groups(progs, true, stream, &launches);
+}
+
+int64_t dionw_newton_schulz_group_launches(int32_t count, const int32_t* kind,
+                                           const int64_t* batch, const int64_t* r,
+                                           const int64_t* c, const int64_t* r_real,
+                                           const int64_t* c_real) {
+  if (count < 0 || count > 4096 || (count > 0 && !(kind && batch && r && c && r_real && c_real)))
+    return -1;
+  // The programs from shapes alone: placeholder addresses, never dereferenced.
+  void* const fake = reinterpret_cast<void*>(uintptr_t{1} << 40);
+  std::vector<std::vector<Problem>> progs(count);
+  for (int i = 0; i < count; ++i) {
+    const size_t need = dionw_newton_schulz_workspace(kind[i], batch[i], r[i], c[i]);
+    if (ns_program(kind[i], batch[i], r[i], c[i], fake, fake, r_real[i], c_real[i], fake, 0,
+                   c[i], r[i] * c[i], fake, need, progs[i]) != kOk)
+      return -1;
+  }
+  int64_t launches = 0;
+  if (walk_groups(progs, false, nullptr, &launches) != kOk) return -1;
+  return launches;
 }
 
 }  // extern "C"

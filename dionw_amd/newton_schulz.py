@@ -22,6 +22,8 @@ from collections.abc import Callable
 from dataclasses import dataclass
 from enum import Enum
 
+import ctypes
+
 import torch
 from torch import Tensor
 
@@ -108,6 +110,58 @@ class HipOrthogonalize:
         return out if matrix.ndim == 3 else out[0]
 
 
+@dataclass(frozen=True)
+class NewtonSchulzCall:
+    """The library arguments of one Newton-Schulz call (see ``newton_schulz_call``)."""
+
+    kind: int
+    blocks: int
+    r: int
+    c: int
+    x: int
+    xt: int
+    r_real: int
+    c_real: int
+    out: int
+    tall: int
+    out_ld: int
+    out_stride: int
+    workspace: int
+    workspace_bytes: int
+
+
+def newton_schulz_call(
+    ortho: HipOrthogonalize,
+    blocks: int,
+    rows: int,
+    cols: int,
+    xr: Tensor,
+    xt: Tensor,
+    out: Tensor,
+    workspace_name: str = "ns_workspace",
+) -> NewtonSchulzCall:
+    """The arguments that iterate on prepared inputs and write ``out`` ([blocks, rows, cols] bf16).
+
+    ``xr`` is the normalized input in the weight's orientation ([blocks,
+    round8(rows), round8(cols)]) and ``xt`` its transpose; a tall block
+    (rows > cols) iterates on the transpose. Both are overwritten. The
+    iteration's workspace is the named scratch buffer ``workspace_name``. The
+    result holds device addresses only: ``xr``, ``xt`` and ``out`` must stay
+    alive until the call has been issued.
+    """
+    tall = rows > cols
+    if tall:
+        x, x_t, r, c, r_real, c_real = xt, xr, _round8(cols), _round8(rows), cols, rows
+    else:
+        x, x_t, r, c, r_real, c_real = xr, xt, _round8(rows), _round8(cols), rows, cols
+    lib = _lib.library()
+    need = int(lib.dionw_newton_schulz_workspace(ortho.lib_kind, blocks, r, c))
+    ws = _workspace.buffer(out.device, workspace_name, (need,), torch.uint8)
+    return NewtonSchulzCall(ortho.lib_kind, blocks, r, c, x.data_ptr(), x_t.data_ptr(), r_real,
+                            c_real, out.data_ptr(), int(tall), cols, rows * cols, ws.data_ptr(),
+                            need)
+
+
 def run_newton_schulz(
     ortho: HipOrthogonalize,
     blocks: int,
@@ -118,22 +172,49 @@ def run_newton_schulz(
     out: Tensor,
     stream: int,
 ) -> None:
-    """Run the iteration on prepared inputs and write ``out`` ([blocks, rows, cols] bf16).
+    """Run the iteration on prepared inputs and write ``out`` (``newton_schulz_call``)."""
+    run_newton_schulz_call(newton_schulz_call(ortho, blocks, rows, cols, xr, xt, out), stream)
 
-    ``xr`` is the normalized input in the weight's orientation ([blocks,
-    round8(rows), round8(cols)]) and ``xt`` its transpose; a tall block
-    (rows > cols) iterates on the transpose. Both are overwritten.
-    """
-    tall = rows > cols
-    if tall:
-        x, x_t, r, c, r_real, c_real = xt, xr, _round8(cols), _round8(rows), cols, rows
-    else:
-        x, x_t, r, c, r_real, c_real = xr, xt, _round8(rows), _round8(cols), rows, cols
-    lib = _lib.library()
-    need = int(lib.dionw_newton_schulz_workspace(ortho.lib_kind, blocks, r, c))
-    ws = _workspace.buffer(out.device, "ns_workspace", (need,), torch.uint8)
-    _lib.call("dionw_newton_schulz", ortho.lib_kind, blocks, r, c, x.data_ptr(), x_t.data_ptr(),
-              r_real, c_real, out.data_ptr(), int(tall), cols, rows * cols, ws.data_ptr(), need,
+
+def run_newton_schulz_call(a: NewtonSchulzCall, stream: int) -> None:
+    """Issue one prepared call (``dionw_newton_schulz``)."""
+    _lib.call("dionw_newton_schulz", a.kind, a.blocks, a.r, a.c, a.x, a.xt, a.r_real, a.c_real,
+              a.out, a.tall, a.out_ld, a.out_stride, a.workspace, a.workspace_bytes, stream)
+
+
+def group_launches(calls: list[NewtonSchulzCall]) -> int:
+    """Product launches one grouped call over ``calls`` issues (from their shapes;
+    ``dionw_newton_schulz_group_launches``)."""
+    n = len(calls)
+
+    def arr(ctype, field):
+        return (ctype * max(n, 1))(*[getattr(c, field) for c in calls])
+
+    launches = int(_lib.library().dionw_newton_schulz_group_launches(
+        n, arr(ctypes.c_int32, "kind"), arr(ctypes.c_int64, "blocks"), arr(ctypes.c_int64, "r"),
+        arr(ctypes.c_int64, "c"), arr(ctypes.c_int64, "r_real"), arr(ctypes.c_int64, "c_real")))
+    if launches < 0:
+        raise ValueError("dionw_newton_schulz_group_launches: invalid run shapes")
+    return launches
+
+
+def run_newton_schulz_group(calls: list[NewtonSchulzCall], stream: int) -> None:
+    """Independent Newton-Schulz calls in grouped launches (``dionw_newton_schulz_group``);
+    their workspaces must be distinct buffers."""
+    if not calls:
+        return
+    n = len(calls)
+
+    def arr(ctype, field):
+        return (ctype * n)(*[getattr(c, field) for c in calls])
+
+    _lib.call("dionw_newton_schulz_group", n, arr(ctypes.c_int32, "kind"),
+              arr(ctypes.c_int64, "blocks"), arr(ctypes.c_int64, "r"), arr(ctypes.c_int64, "c"),
+              arr(ctypes.c_void_p, "x"), arr(ctypes.c_void_p, "xt"),
+              arr(ctypes.c_int64, "r_real"), arr(ctypes.c_int64, "c_real"),
+              arr(ctypes.c_void_p, "out"), arr(ctypes.c_int32, "tall"),
+              arr(ctypes.c_int64, "out_ld"), arr(ctypes.c_int64, "out_stride"),
+              arr(ctypes.c_void_p, "workspace"), arr(ctypes.c_size_t, "workspace_bytes"),
               stream)
 
 

@@ -33,7 +33,13 @@ from dionw_amd._keys import (
     ROW_NORMALIZATION_KEY,
     STRUCTURAL_KEYS,
 )
-from dionw_amd._matrix_step import MAX_RUN_ELEMENTS, run_elements, step_run
+from dionw_amd._matrix_step import (
+    ACTIVE_RUNS,
+    MAX_RUN_ELEMENTS,
+    RunQueue,
+    run_elements,
+    step_run,
+)
 from dionw_amd.ema._fusion import ACTIVE_EMA
 from dionw_amd.ema import EMAConfig, IntegratedEMAOptimizer, ProfileRegion, no_profile
 from dionw_amd.matrix_update import DION3_UPDATE, MatrixUpdate, MomentumForm, RowNormalization
@@ -217,13 +223,19 @@ class _DionCore(Optimizer):
                 loss = closure()
         # A due GPU EMA update can ride on the passes that write the new weights.
         token = ACTIVE_EMA.set(getattr(self, "ema", None))
+        # Bucket runs queue after their momentum passes; their Newton-Schulz
+        # calls then run as grouped launches.
+        queue = RunQueue()
+        runs_token = ACTIVE_RUNS.set(queue)
         try:
             for bucket in self._ensure_buckets():
                 self._step_bucket(bucket)
+            queue.flush()
             for group in self.param_groups:
                 if RouteKind(group[ROUTE_KEY]) is RouteKind.ADAMW:
                     adamw_step(group, self.state)
         finally:
+            ACTIVE_RUNS.reset(runs_token)
             ACTIVE_EMA.reset(token)
         return loss
 

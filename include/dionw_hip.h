@@ -136,6 +136,37 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
                         size_t workspace_bytes, dionw_stream_t stream);
 
 /*
+ * dionw_newton_schulz for count independent bucket runs at once: element i of
+ * every array is run i's argument. Runs whose product sequences match (same
+ * kind and shape class) execute together, up to 8 at a time, one launch per
+ * product of the sequence, so that small runs fill the CUs a large run's
+ * launches leave idle. Results are bit-identical to count separate calls.
+ * The runs' workspaces must not overlap (checked); all arguments are checked
+ * before anything is launched. Replaces the per-run orthogonalize calls of a
+ * step (_matrix_step.py:254-265, one per run of optimizer.py:351-369).
+ */
+int dionw_newton_schulz_group(int32_t count, const int32_t* kind, const int64_t* batch,
+                              const int64_t* r, const int64_t* c, void* const* x,
+                              void* const* xt, const int64_t* r_real, const int64_t* c_real,
+                              void* const* out, const int32_t* out_transposed,
+                              const int64_t* out_ld, const int64_t* out_stride,
+                              void* const* workspace, const size_t* workspace_bytes,
+                              dionw_stream_t stream);
+
+/*
+ * Product launches dionw_newton_schulz_group would issue for runs of these
+ * shapes (which of their products it groups), or -1 for invalid arguments;
+ * nothing is launched and no memory is touched. For one run it is the length
+ * of that run's product sequence. Callers use it to keep runs apart when
+ * grouping would save nothing (each run's passes then follow its own
+ * iteration while its output is still in cache).
+ */
+int64_t dionw_newton_schulz_group_launches(int32_t count, const int32_t* kind,
+                                           const int64_t* batch, const int64_t* r,
+                                           const int64_t* c, const int64_t* r_real,
+                                           const int64_t* c_real);
+
+/*
  * NorMuon statistics of the orthogonalized rows O (bf16 [blocks, k, cols]):
  * v = lerp(v, mean(O^2), 1 - beta2) written back into variance [blocks, rows]
  * at the selected rows (idx [blocks, k], or every row when idx == NULL),

@@ -33,6 +33,66 @@ def test_library_exports_every_declared_symbol() -> None:
     assert _lib.library().dionw_abi_version() == 1
 
 
+def test_grouped_newton_schulz_rejects_overlapping_workspaces() -> None:
+    """Runs of one grouped call execute together, so their workspaces must be
+    disjoint; the host rejects the call before any launch (the fake device
+    addresses below are never dereferenced)."""
+    n = 2
+    need = int(_lib.library().dionw_newton_schulz_workspace(0, 1, 64, 128))
+    base = 1 << 40
+
+    def arr(ctype, *values):
+        return (ctype * n)(*values)
+
+    i32, i64, ptr = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+    args = [arr(i32, 0, 0), arr(i64, 1, 1), arr(i64, 64, 64), arr(i64, 128, 128),
+            arr(ptr, base, base + 2**30), arr(ptr, base + 2**31, base + 2**32),
+            arr(i64, 64, 64), arr(i64, 128, 128), arr(ptr, base + 2**33, base + 2**34),
+            arr(i32, 0, 0), arr(i64, 128, 128), arr(i64, 64 * 128, 64 * 128)]
+    with pytest.raises(ValueError, match="overlap"):
+        _lib.call("dionw_newton_schulz_group", n, *args,
+                  arr(ptr, base + 2**35, base + 2**35 + need // 2),
+                  arr(ctypes.c_size_t, need, need), None)
+    with pytest.raises(ValueError, match="bad count"):
+        _lib.call("dionw_newton_schulz_group", -1, *args, arr(ptr, base, base),
+                  arr(ctypes.c_size_t, 0, 0), None)
+
+
+def _planned_launches(runs: list[tuple[int, int, int, int]]) -> int:
+    """dionw_newton_schulz_group_launches for (kind, blocks, rows, cols) runs (wide)."""
+    n = len(runs)
+
+    def arr(ctype, values):
+        return (ctype * max(n, 1))(*values)
+
+    kinds, blocks = [r[0] for r in runs], [r[1] for r in runs]
+    rows, cols = [r[2] for r in runs], [r[3] for r in runs]
+    i64 = ctypes.c_int64
+    return _lib.library().dionw_newton_schulz_group_launches(
+        n, arr(ctypes.c_int32, kinds), arr(i64, blocks), arr(i64, rows), arr(i64, cols),
+        arr(i64, rows), arr(i64, cols))
+
+
+def test_grouping_plan() -> None:
+    """Which products the grouped call merges, from shapes alone (no GPU needed).
+
+    Llama-3-8B's four runs share their 14 symmetric and 2 syrk products (the
+    Q X products already fill whole rounds alone); the MoE runs' products stay
+    apart (their r = 352 side is not a multiple of 64, and grouping the others
+    would replace better-fitting 128 x 128 tiles); GPT-2's three Gram runs share
+    every product and its square block keeps its own 15.
+    """
+    llama = [(0, 64, 1024, 4096), (0, 64, 256, 4096), (0, 64, 3584, 4096), (0, 32, 1024, 14336)]
+    assert [_planned_launches([r]) for r in llama] == [18] * 4
+    assert _planned_launches(llama) == 24
+    assert _planned_launches([(0, 128, 352, 2048), (0, 64, 512, 1408)]) == 36
+    gpt2 = [(0, 12, 768, 2304), (0, 12, 768, 768), (0, 12, 768, 3072), (0, 12, 768, 3072)]
+    assert _planned_launches(gpt2) == 18 + 15
+    assert _planned_launches([(1, 4, 256, 1024), (2, 4, 256, 1024)]) == 15  # both bf16 quintics
+    assert _planned_launches([(7, 1, 64, 128)]) == -1
+    assert _planned_launches([]) == 0
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path) -> None:
     monkeypatch.setattr(_lib, "_PATH", tmp_path / "absent.so")
     monkeypatch.setattr(_lib, "_LIB", None)
