@@ -290,30 +290,60 @@ def cpu_baseline(spec, fraction: float, threads: int) -> dict:
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 
+# The Newton-Schulz runs of one Llama-3-8B step: (blocks, selected rows, cols).
+LLAMA_NS_RUNS = [(64, 1024, 4096), (64, 256, 4096), (64, 3584, 4096), (32, 1024, 14336)]
+
+
+def ns_algorithmic_bytes(blocks: int, r: int, c: int) -> float:
+    """HBM bytes the 18 products of one Gram iteration must move for a run of
+    ``blocks`` r x c blocks (16-bit data; per product each operand read once,
+    each output written once): 2 syrks (X read, G written), 5 polynomials (G
+    read, Z written; twice Q = Z + aI too), 3 Q and 6 Gram updates (two
+    operands read, one written) and 2 Q X products (Q and X^T read, X written;
+    at the restart X^T too): 7 r c + 43 r^2 elements per block."""
+    return 2.0 * blocks * (7.0 * r * c + 43.0 * r * r)
+
+
 def traffic_bytes():
-    """HBM bytes per launch of the dominant product, from the committed
-    FETCH_SIZE / WRITE_SIZE measurement (``--probe`` under rocprofv3 --pmc), or None."""
+    """Average HBM bytes per Newton-Schulz product launch of the Llama-3-8B
+    step, from the committed FETCH_SIZE / WRITE_SIZE measurement (``--probe``
+    under rocprofv3 --pmc), or None."""
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
-        return data["gemm_sym_r3584"]["hbm_bytes_per_launch"]
+        return data["ns_step"]["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
 
 
 def probe() -> int:
-    """One launch of each kernel whose traffic is measured, plus a copy of known
-    size for calibrating the counters (run under ``rocprofv3 --pmc``)."""
+    """The launches whose traffic is measured (run under ``rocprofv3 --pmc``): a
+    copy of known size for calibrating the counters, the grouped Newton-Schulz
+    call of one Llama-3-8B step (its 24 product launches) and one accumulate
+    pass over a gate/up-sized run."""
     import torch
 
-    from dionw_amd import _kernels, _lib
+    from dionw_amd import _lib
+    from dionw_amd.newton_schulz import (
+        NewtonSchulz,
+        newton_schulz_call,
+        newton_schulz_fn,
+        run_newton_schulz_group,
+    )
 
     dev = torch.device("cuda:0")
     src = torch.empty(256 * 2**20, device=dev)  # 1 GiB of float32
     dst = torch.empty_like(src)
     dst.copy_(src)
-    g = torch.randn(18, 3584, 3584, device=dev).half()
-    z = torch.empty_like(g)
-    _kernels.gemm_nt(g, g, d=g, alpha=0.5, beta=-1.5, out=z, symmetric=True)
+    ortho = newton_schulz_fn(NewtonSchulz.GRAM)
+    calls, buffers = [], []
+    for i, (blocks, r, c) in enumerate(LLAMA_NS_RUNS):
+        x = (torch.randn(blocks, r, c, device=dev) / math.sqrt(r * c)).half()
+        xt = x.mT.contiguous()
+        out = torch.empty(blocks, r, c, device=dev, dtype=torch.bfloat16)
+        buffers += [x, xt, out]
+        calls.append(newton_schulz_call(ortho, blocks, r, c, x, xt, out, f"probe_ns#{i}"))
+    run_newton_schulz_group(calls, _lib.stream_handle(dev))
+    del buffers
     grads = [torch.randn(14336, 4096, device=dev) * 1e-3 for _ in range(18)]
     mom = torch.zeros(18 * 14336, 4096, device=dev)
     scores = torch.empty(18 * 14336, device=dev)
@@ -321,7 +351,8 @@ def probe() -> int:
     _lib.call("dionw_accumulate_scores", _lib.ptr_array(grads), 18, 14336, 4096, mom.data_ptr(),
               scores.data_ptr(), rowsq.data_ptr(), _lib.stream_handle(dev))
     torch.cuda.synchronize()
-    print("probe done: copy 1 GiB, gemm_nt sym 18x3584^2 k=3584, accumulate 18x14336x4096")
+    print("probe done: copy 1 GiB, grouped Newton-Schulz of the Llama-3-8B runs, "
+          "accumulate 18x14336x4096")
     return 0
 
 
