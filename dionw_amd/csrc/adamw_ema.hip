@@ -98,29 +98,31 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamTable t, AdamScalars s, 
         mv[e] = me;
         vv[e] = ve;
       }
-      p4[q] = pv;
-      m4[q] = mv;
-      v4[q] = vv;
+      __builtin_nontemporal_store(pv, p4 + q);
+      __builtin_nontemporal_store(mv, m4 + q);
+      __builtin_nontemporal_store(vv, v4 + q);
       if (EMA) {
         f32x4* s4 = reinterpret_cast<f32x4*>(sh);
-        f32x4 sv = s4[q];
+        f32x4 sv = __builtin_nontemporal_load(s4 + q);
 #pragma unroll
         for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], pv[e], ema_weight);
-        s4[q] = sv;
+        __builtin_nontemporal_store(sv, s4 + q);
       }
     };
+    // Every element is read once and written once: streaming (non-temporal)
+    // loads and stores move this traffic faster than cached ones.
+    auto ld = [](const f32x4* x) { return __builtin_nontemporal_load(x); };
     const int64_t n4 = end >> 2;
     int64_t q = threadIdx.x;
     // Two chunks per iteration: eight 16-byte loads in flight per lane.
     for (; q + 256 < n4; q += 512) {
-      const f32x4 pa = p4[q], pb = p4[q + 256];
-      const f32x4 ga = __builtin_nontemporal_load(g4 + q);
-      const f32x4 gb = __builtin_nontemporal_load(g4 + q + 256);
-      const f32x4 ma = m4[q], mb = m4[q + 256], va = v4[q], vb = v4[q + 256];
+      const f32x4 pa = ld(p4 + q), pb = ld(p4 + q + 256);
+      const f32x4 ga = ld(g4 + q), gb = ld(g4 + q + 256);
+      const f32x4 ma = ld(m4 + q), mb = ld(m4 + q + 256), va = ld(v4 + q), vb = ld(v4 + q + 256);
       update(q, pa, ga, ma, va);
       update(q + 256, pb, gb, mb, vb);
     }
-    for (; q < n4; q += 256) update(q, p4[q], __builtin_nontemporal_load(g4 + q), m4[q], v4[q]);
+    for (; q < n4; q += 256) update(q, ld(p4 + q), ld(g4 + q), ld(m4 + q), ld(v4 + q));
     i = end & ~(int64_t)3;
   }
   for (int64_t e = i + threadIdx.x; e < end; e += 256) {
@@ -164,15 +166,17 @@ __global__ __launch_bounds__(256) void ema_kernel(EmaTable t, float weight) {
   const bool vec = ((reinterpret_cast<uintptr_t>(s) | reinterpret_cast<uintptr_t>(p)) & 15) == 0;
   int64_t i = 0;
   if (vec) {
+    // Streaming (non-temporal) accesses: each element is touched once.
+    f32x4* s4 = reinterpret_cast<f32x4*>(s);
     for (int64_t q = threadIdx.x; 4 * q + 3 < end; q += 256) {
-      const f32x4 pv = reinterpret_cast<const f32x4*>(p)[q];
+      const f32x4 pv = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + q);
       if (COPY) {
-        reinterpret_cast<f32x4*>(s)[q] = pv;
+        __builtin_nontemporal_store(pv, s4 + q);
       } else {
-        f32x4 sv = reinterpret_cast<f32x4*>(s)[q];
+        f32x4 sv = __builtin_nontemporal_load(s4 + q);
 #pragma unroll
         for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], pv[e], weight);
-        reinterpret_cast<f32x4*>(s)[q] = sv;
+        __builtin_nontemporal_store(sv, s4 + q);
       }
     }
     i = end & ~(int64_t)3;

@@ -135,6 +135,8 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
   const bool apply_decay = a.apply_decay != 0;
   constexpr int U = 4;  // chunks whose loads are issued together
   constexpr int T = kApplyThreads;
+  // Every element is read once and written once: the vector paths stream
+  // (non-temporal loads and stores), which moves this traffic faster.
   if (slot < 0) {
     if (!apply_decay && !EMA) return;
     // Rows outside the selection: W = W d (weight decay) and, with the EMA,
@@ -142,14 +144,14 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
     auto row_end = [&](f32x4 wv, int64_t c) {
       if (apply_decay) {
         wv = wv * a.decay;
-        reinterpret_cast<f32x4*>(w)[c] = wv;
+        __builtin_nontemporal_store(wv, reinterpret_cast<f32x4*>(w) + c);
       }
       if (EMA) {
         f32x4* s4 = reinterpret_cast<f32x4*>(sh);
-        f32x4 sv = s4[c];
+        f32x4 sv = __builtin_nontemporal_load(s4 + c);
 #pragma unroll
         for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], wv[e], a.ema_weight);
-        s4[c] = sv;
+        __builtin_nontemporal_store(sv, s4 + c);
       }
     };
     if (a.vec) {
@@ -159,11 +161,11 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
       for (; c + (U - 1) * T < n4; c += U * T) {
         f32x4 wv[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) wv[u] = w4[c + u * T];
+        for (int u = 0; u < U; ++u) wv[u] = __builtin_nontemporal_load(w4 + c + u * T);
 #pragma unroll
         for (int u = 0; u < U; ++u) row_end(wv[u], c + u * T);
       }
-      for (; c < n4; c += T) row_end(w4[c], c);
+      for (; c < n4; c += T) row_end(__builtin_nontemporal_load(w4 + c), c);
     } else {
       for (int64_t c = tid; c < a.cols; c += T) {
         float wv = w[c];
@@ -188,13 +190,13 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
       return wv;
     };
     auto store = [&](int64_t c, f32x4 wv) {
-      w4[c] = wv;
+      __builtin_nontemporal_store(wv, w4 + c);
       if (EMA) {
         f32x4* s4 = reinterpret_cast<f32x4*>(sh);
-        f32x4 sv = s4[c];
+        f32x4 sv = __builtin_nontemporal_load(s4 + c);
 #pragma unroll
         for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], wv[e], a.ema_weight);
-        s4[c] = sv;
+        __builtin_nontemporal_store(sv, s4 + c);
       }
     };
     const int64_t n4 = a.cols >> 2;
@@ -204,13 +206,14 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
       bf16x4 ov[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        wv[u] = w4[c + u * T];
-        ov[u] = o4[c + u * T];
+        wv[u] = __builtin_nontemporal_load(w4 + c + u * T);
+        ov[u] = __builtin_nontemporal_load(o4 + c + u * T);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) store(c + u * T, upd(wv[u], ov[u]));
     }
-    for (; c < n4; c += T) store(c, upd(w4[c], o4[c]));
+    for (; c < n4; c += T)
+      store(c, upd(__builtin_nontemporal_load(w4 + c), __builtin_nontemporal_load(o4 + c)));
   } else {
     for (int64_t c = tid; c < a.cols; c += T) {
       const float wv = update_one(w[c], (float)o[c], d, s, normalized, a.decay, apply_decay);
