@@ -112,8 +112,14 @@ class Timeline:
                 count, rows, cols = a[1], a[2], a[3]
                 entry["bytes"] += 12.0 * count * rows * cols
             elif name == "dionw_prepare_ns_input":
-                blocks, cols, k = a[5], a[7], a[8]
-                entry["bytes"] += 12.0 * blocks * k * cols
+                # per element: M read (if any) and written (write_m), G read in
+                # every-row mode (no idx), the 16-bit (or float32) input and its transpose
+                momentum, idx, blocks, cols, k = a[2], a[3], a[5], a[7], a[8]
+                write_m, elem, transposed = a[13], a[14], a[16]
+                out_bytes = 4.0 if elem == 2 else 2.0
+                per = ((4.0 if momentum else 0.0) + (4.0 if momentum and write_m else 0.0)
+                       + (4.0 if idx is None else 0.0) + out_bytes * (2 if transposed else 1))
+                entry["bytes"] += per * blocks * k * cols
             elif name == "dionw_apply_update":
                 count, bpt, rows, cols, k, decay_on = a[1], a[2], a[3], a[4], a[5], a[13]
                 n = count * bpt * rows * cols
