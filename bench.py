@@ -113,12 +113,14 @@ class Timeline:
                 entry["bytes"] += 12.0 * count * rows * cols
             elif name == "dionw_prepare_ns_input":
                 # per element: M read (if any) and written (write_m), G read in
-                # every-row mode (no idx), the 16-bit (or float32) input and its transpose
+                # every-row mode (no idx), the 16-bit (or float32) input in each
+                # orientation written
                 momentum, idx, blocks, cols, k = a[2], a[3], a[5], a[7], a[8]
-                write_m, elem, transposed = a[13], a[14], a[16]
+                write_m, elem, rowmajor, transposed = a[13], a[14], a[15], a[16]
                 out_bytes = 4.0 if elem == 2 else 2.0
                 per = ((4.0 if momentum else 0.0) + (4.0 if momentum and write_m else 0.0)
-                       + (4.0 if idx is None else 0.0) + out_bytes * (2 if transposed else 1))
+                       + (4.0 if idx is None else 0.0)
+                       + out_bytes * ((1 if rowmajor else 0) + (1 if transposed else 0)))
                 entry["bytes"] += per * blocks * k * cols
             elif name == "dionw_apply_update":
                 count, bpt, rows, cols, k, decay_on = a[1], a[2], a[3], a[4], a[5], a[13]
@@ -305,9 +307,10 @@ def ns_algorithmic_bytes(blocks: int, r: int, c: int) -> float:
     ``blocks`` r x c blocks (16-bit data; per product each operand read once,
     each output written once): 2 syrks (X read, G written), 5 polynomials (G
     read, Z written; twice Q = Z + aI too), 3 Q and 6 Gram updates (two
-    operands read, one written) and 2 Q X products (Q and X^T read, X written;
-    at the restart X^T too): 7 r c + 43 r^2 elements per block."""
-    return 2.0 * blocks * (7.0 * r * c + 43.0 * r * r)
+    operands read, one written) and 2 Q X products (Q and X read, X written):
+    6 r c + 43 r^2 elements per block. Where r is not a multiple of 32 the Q X
+    products read X^T instead and the restart writes X^T too: 7 r c."""
+    return 2.0 * blocks * ((6.0 if r % 32 == 0 else 7.0) * r * c + 43.0 * r * r)
 
 
 def traffic_bytes():
@@ -333,6 +336,7 @@ def probe() -> int:
         NewtonSchulz,
         newton_schulz_call,
         newton_schulz_fn,
+        prepared_orientations,
         run_newton_schulz_group,
     )
 
@@ -344,7 +348,8 @@ def probe() -> int:
     calls, buffers = [], []
     for i, (blocks, r, c) in enumerate(LLAMA_NS_RUNS):
         x = (torch.randn(blocks, r, c, device=dev) / math.sqrt(r * c)).half()
-        xt = x.mT.contiguous()
+        # Like the optimizer step, only the inputs the iteration reads.
+        xt = x.mT.contiguous() if prepared_orientations(r, c)[1] else None
         out = torch.empty(blocks, r, c, device=dev, dtype=torch.bfloat16)
         buffers += [x, xt, out]
         calls.append(newton_schulz_call(ortho, blocks, r, c, x, xt, out, f"probe_ns#{i}"))

@@ -49,6 +49,8 @@ from dionw_amd.newton_schulz import (
     NewtonSchulzCall,
     group_launches,
     newton_schulz_call,
+    prepared_inputs,
+    prepared_orientations,
     run_newton_schulz,
     run_newton_schulz_call,
     run_newton_schulz_group,
@@ -63,7 +65,7 @@ NEWTON_SCHULZ_EPS: Final[float] = 1e-8
 # Largest update (blocks x selected rows x cols) one run orthogonalizes at once.
 # The reference caps runs at 2**28 to bound several float32 copies of the update
 # on smaller GPUs (_matrix_step.py:40-50). The fused passes here hold no float32
-# copy: a run keeps its selected rows in fp16 (row-major and transposed), the
+# copy: a run keeps its selected rows in fp16 (in one or both orientations), the
 # bf16 output and the Newton-Schulz workspace (six fp16 r x r matrices and one
 # r x c per block): at most 20 bytes per update element (square blocks), under
 # 22 GB at this cap (17 GB for the Llama-3-8B gate/up bucket). Bigger runs fill
@@ -187,7 +189,8 @@ def _ns_bytes(ortho: HipOrthogonalize, blocks: int, k: int, cols: int) -> int:
     p_pad, j_pad = _round8(k), _round8(cols)
     r, c = min(p_pad, j_pad), max(p_pad, j_pad)
     work = int(_lib.library().dionw_newton_schulz_workspace(ortho.lib_kind, blocks, r, c))
-    return 2 * 2 * blocks * p_pad * j_pad + 2 * blocks * k * cols + work
+    inputs = sum(prepared_orientations(k, cols))
+    return inputs * 2 * blocks * p_pad * j_pad + 2 * blocks * k * cols + work
 
 
 def step_run(
@@ -243,12 +246,12 @@ def step_run(
     idx_ptr = None if idx is None else idx.data_ptr()
 
     if fused:
-        p_pad, j_pad = _round8(k), _round8(cols)
-        xr = _workspace.buffer(device, "ns_xr" + own, (blocks, p_pad, j_pad), ortho.dtype)
-        xt = _workspace.buffer(device, "ns_xt" + own, (blocks, j_pad, p_pad), ortho.dtype)
+        # Only the orientations the iteration reads are written.
+        xr, xt = prepared_inputs(ortho, device, blocks, k, cols, "ns_xr" + own, "ns_xt" + own)
         _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
-                  den.data_ptr(), blocks, rows, cols, k, p_pad, j_pad, mu, int(nesterov), 1,
-                  ortho.elem, xr.data_ptr(), xt.data_ptr(), stream)
+                  den.data_ptr(), blocks, rows, cols, k, _round8(k), _round8(cols), mu,
+                  int(nesterov), 1, ortho.elem, None if xr is None else xr.data_ptr(),
+                  None if xt is None else xt.data_ptr(), stream)
         orthogonal = _workspace.buffer(device, "ns_out" + own, (blocks, k, cols), torch.bfloat16)
         if queue is not None:
             call = newton_schulz_call(ortho, blocks, k, cols, xr, xt, orthogonal,

@@ -48,6 +48,7 @@ struct GemmArgs {
   int sym;
   int ct_vec;           // transposed store may use 8-byte vectors
   int tiles_m, tiles_n;
+  int b_kn;             // B given as [k, n] (row-major along n) instead of [n, k]
 };
 
 struct Problem {
@@ -499,8 +500,17 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16* lds_v4i16_t;
+
 // One output tile: logical tile w of the problem (batch index w / tiles).
-template <typename T, typename OUT_T, int MODE, typename CFG>
+// BKN: B is [k, n] (row-major along n, such as the iterate X of Q X) instead
+// of [n, k]. Its stages are then k-major in LDS, [k][n], with 16-byte chunk ch
+// of row k at ch ^ (4 * (k % 4)), and each B fragment is two transpose reads
+// (ds_read_b64_tr_b16): a lane of a 16-lane group addressing row base + i / 4,
+// columns 4 (i % 4) .. + 3 hands lane i column i, rows base .. base + 3. With the
+// swizzle, a half-wave's 32 reads hit 16 distinct 16-byte bank groups.
+template <typename T, typename OUT_T, int MODE, typename CFG, bool BKN>
 __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
   constexpr int PBM = CFG::BM, PBN = CFG::BN, PWN = CFG::WN, PSTAGES = CFG::STAGES;
   constexpr int PSTAGE_ELEMS = CFG::stage_elems, LA = CFG::loads_a, LB = CFG::loads_b;
@@ -541,12 +551,20 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
     const int row = pos / CPR, logical = swz<SBK>(row, pos % CPR);
     a_src[j] = A + (int64_t)min(m0 + row, g.m - 1) * g.lda + logical * 8;
   }
+  constexpr int NCH = PBN / 8;  // 16-byte chunks per k-row of a k-major B stage
 #pragma unroll
   for (int j = 0; j < LB; ++j) {
     const int pos = (wave * LB + j) * 64 + lane;
-    const int row = pos / CPR, logical = swz<SBK>(row, pos % CPR);
-    b_src[j] = B + (int64_t)min(n0 + row, g.n - 1) * g.ldb + logical * 8;
+    if (BKN) {
+      // Columns past n load a clamped valid chunk (n is a multiple of 8).
+      const int krow = pos / NCH, ch = (pos % NCH) ^ (4 * (krow % 4));
+      b_src[j] = B + (int64_t)krow * g.ldb + min(n0 + ch * 8, g.n - 8);
+    } else {
+      const int row = pos / CPR, logical = swz<SBK>(row, pos % CPR);
+      b_src[j] = B + (int64_t)min(n0 + row, g.n - 1) * g.ldb + logical * 8;
+    }
   }
+  const int64_t b_step = BKN ? (int64_t)SBK * g.ldb : SBK;  // B elements per stage
   auto issue = [&](int kt) {
     T* stage = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
     const int k0 = kt * SBK;
@@ -556,7 +574,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
                                        (lds_ptr_t)(stage + (wave * LA + j) * 512), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < LB; ++j)
-      __builtin_amdgcn_global_load_lds((const void*)(b_src[j] + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(b_src[j] + kt * b_step),
                                        (lds_ptr_t)(stage + PBM * SBK + (wave * LB + j) * 512), 16,
                                        0, 0);
   };
@@ -592,8 +610,24 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
       for (int i = 0; i < FM; ++i)
         af[set][i] = *reinterpret_cast<const V*>(As + plds_off<SBK>(wm * WTM + i * 32 + lrow, 2 * ks + lk));
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bfr[set][j] = *reinterpret_cast<const V*>(Bs + plds_off<SBK>(wn * WTN + j * 32 + lrow, 2 * ks + lk));
+      for (int j = 0; j < FN; ++j) {
+        if (BKN) {
+          const int G = lane >> 4, i16 = lane & 15;
+          const int col = wn * WTN + j * 32 + 16 * (G & 1) + 4 * (i16 & 3);
+          v4i16 half[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int krow = ks * 16 + 8 * (G >> 1) + 4 * h + (i16 >> 2);
+            const int ch = (col >> 3) ^ (4 * (krow & 3));
+            half[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_v4i16_t)(Bs + krow * PBN + ch * 8 + (col & 7)));
+          }
+          bfr[set][j] = __builtin_bit_cast(
+              V, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        } else {
+          bfr[set][j] = *reinterpret_cast<const V*>(Bs + plds_off<SBK>(wn * WTN + j * 32 + lrow, 2 * ks + lk));
+        }
+      }
     };
     frag(0, 0);
 #pragma unroll
@@ -627,9 +661,9 @@ __device__ __forceinline__ int tile_count(const GemmArgs& g) {
   return g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
 }
 
-template <typename T, typename OUT_T, int MODE, typename CFG>
+template <typename T, typename OUT_T, int MODE, typename CFG, bool BKN>
 __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs g, int batch) {
-  pipe_tile<T, OUT_T, MODE, CFG>(g, xcd_tile((int)blockIdx.x, tile_count(g) * batch));
+  pipe_tile<T, OUT_T, MODE, CFG, BKN>(g, xcd_tile((int)blockIdx.x, tile_count(g) * batch));
 }
 
 // Several independent products in one launch (the same product of several
@@ -644,7 +678,7 @@ struct GemmGroup {
   int count;
 };
 
-template <typename T, typename OUT_T, int MODE, typename CFG>
+template <typename T, typename OUT_T, int MODE, typename CFG, bool BKN>
 __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_group_kernel(GemmGroup grp) {
   int q = 0;
   for (int j = 1; j < grp.count; ++j)
@@ -652,7 +686,7 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_group_kernel(Gem
   const GemmArgs& g = grp.g[q];
   const int w = xcd_tile((int)blockIdx.x - grp.start[q], tile_count(g) * grp.batch[q]);
   if (w < 0) return;  // the whole workgroup: w depends on blockIdx only
-  pipe_tile<T, OUT_T, MODE, CFG>(g, w);
+  pipe_tile<T, OUT_T, MODE, CFG, BKN>(g, w);
 }
 
 // ---- launch configuration ----------------------------------------------------
@@ -742,10 +776,10 @@ int allow_lds(size_t lds_bytes) {
   return kOk;
 }
 
-template <typename T, typename OUT_T, int MODE, typename CFG>
-int launch_pipe(const Problem& p, hipStream_t stream) {
+template <typename T, typename OUT_T, int MODE, typename CFG, bool BKN>
+int launch_pipe_kn(const Problem& p, hipStream_t stream) {
   constexpr size_t lds_bytes = pipe_lds_bytes<CFG>();
-  constexpr auto kern = gemm_nt_pipe_kernel<T, OUT_T, MODE, CFG>;
+  constexpr auto kern = gemm_nt_pipe_kernel<T, OUT_T, MODE, CFG, BKN>;
   DIONW_TRY(allow_lds<kern>(lds_bytes));
   GemmArgs g;
   const int64_t wgs = pipe_args<CFG>(p, g);
@@ -755,13 +789,19 @@ int launch_pipe(const Problem& p, hipStream_t stream) {
   return check_launch("gemm_nt_pipe");
 }
 
+template <typename T, typename OUT_T, int MODE, typename CFG>
+int launch_pipe(const Problem& p, hipStream_t stream) {
+  if (p.g.b_kn) return launch_pipe_kn<T, OUT_T, MODE, CFG, true>(p, stream);
+  return launch_pipe_kn<T, OUT_T, MODE, CFG, false>(p, stream);
+}
+
 // One launch of up to kMaxGroup products on 256x256 tiles with 64-deep stages,
 // longest k first (its tiles take longest, so they start first).
-template <typename T, typename OUT_T, int MODE>
-int launch_pipe_group(const std::vector<const Problem*>& ps, hipStream_t stream) {
+template <typename T, typename OUT_T, int MODE, bool BKN>
+int launch_pipe_group_kn(const std::vector<const Problem*>& ps, hipStream_t stream) {
   using Big64 = PipeCfg<256, 256, 4, 4, 2, 64>;
   constexpr size_t lds_bytes = pipe_lds_bytes<Big64>();
-  constexpr auto kern = gemm_nt_pipe_group_kernel<T, OUT_T, MODE, Big64>;
+  constexpr auto kern = gemm_nt_pipe_group_kernel<T, OUT_T, MODE, Big64, BKN>;
   DIONW_TRY(allow_lds<kern>(lds_bytes));
   std::vector<const Problem*> order(ps);
   std::stable_sort(order.begin(), order.end(),
@@ -782,6 +822,12 @@ int launch_pipe_group(const std::vector<const Problem*>& ps, hipStream_t stream)
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)start), dim3(Big64::threads), lds_bytes, stream, grp);
   return check_launch("gemm_nt_pipe_group");
+}
+
+template <typename T, typename OUT_T, int MODE>
+int launch_pipe_group(const std::vector<const Problem*>& ps, hipStream_t stream) {
+  if (ps[0]->g.b_kn) return launch_pipe_group_kn<T, OUT_T, MODE, true>(ps, stream);
+  return launch_pipe_group_kn<T, OUT_T, MODE, false>(ps, stream);
 }
 
 // Workgroups a tile size yields (symmetric products: upper-triangle tiles).
@@ -810,6 +856,10 @@ int launch_typed(const Problem& p, hipStream_t stream) {
   using Big32 = PipeCfg<256, 256, 4, 4, 4, 32>;
   using Mid32 = PipeCfg<128, 128, 2, 2, 4, 32>;
   const bool k64 = p.g.k % 64 == 0, k32 = p.g.k % 32 == 0;
+  if (p.g.b_kn && !k32) {
+    set_error("gemm: a [k, n] B operand needs k to be a multiple of 32");
+    return kInvalid;
+  }
 #ifdef DIONW_FORCE_KERNEL
   // Tuning builds only: one tile shape for every product it can run.
   if (DIONW_FORCE_KERNEL == 1 && k32) {
@@ -820,8 +870,8 @@ int launch_typed(const Problem& p, hipStream_t stream) {
     if (k64) return launch_pipe<T, OUT_T, MODE, Mid64>(p, stream);
     return launch_pipe<T, OUT_T, MODE, Mid32>(p, stream);
   }
-  if (DIONW_FORCE_KERNEL == 3) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
-  if (DIONW_FORCE_KERNEL == 4) return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
+  if (DIONW_FORCE_KERNEL == 3 && !p.g.b_kn) return launch_cfg<T, OUT_T, 128, 128, 2, 2, MODE>(p, stream);
+  if (DIONW_FORCE_KERNEL == 4 && !p.g.b_kn) return launch_cfg<T, OUT_T, 64, 64, 2, 2, MODE>(p, stream);
 #endif
   if (k32) {
     // The smaller tile wins when the big one leaves CUs idle or pads a ragged side.
@@ -847,6 +897,10 @@ int launch(const Problem& p, hipStream_t stream) {
   if (!operands_ok(g)) {
     set_error("gemm: k, operand row strides and batch strides must be multiples of 8 "
               "elements and operands 16-byte aligned");
+    return kInvalid;
+  }
+  if (g.b_kn && (g.n % 8 || g.sym)) {
+    set_error("gemm: a [k, n] B operand needs n to be a multiple of 8 (and no symmetric mode)");
     return kInvalid;
   }
   if (p.elem == kF16) {
@@ -890,7 +944,8 @@ bool groups(const std::vector<const Problem*>& live) {
   bool together = live.size() >= 2 && live.size() <= (size_t)kMaxGroup;
   for (const Problem* p : live)
     together = together && p->elem == live[0]->elem && p->out_mode == live[0]->out_mode &&
-               p->g.k % 64 == 0 && p->batch <= INT32_MAX && operands_ok(p->g);
+               p->g.b_kn == live[0]->g.b_kn && p->g.k % 64 == 0 && p->batch <= INT32_MAX &&
+               operands_ok(p->g) && !(p->g.b_kn && (p->g.n % 8 || p->g.sym));
   return together && group_pays(live);
 }
 
@@ -1058,7 +1113,10 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
                std::vector<Problem>& prog) {
   DIONW_REQUIRE(kind == kGram || kind == kPolarExpress || kind == kKeller,
                 "newton_schulz: unknown kind %d", kind);
-  DIONW_REQUIRE(x && xt && out && workspace, "newton_schulz: null pointer");
+  // With r a multiple of 32 the products that multiply X from the left read
+  // it directly as a [k, n] operand, so xt is neither read nor written.
+  const bool direct = r % 32 == 0;
+  DIONW_REQUIRE(x && (xt || direct) && out && workspace, "newton_schulz: null pointer");
   DIONW_REQUIRE(r > 0 && c >= r && r % 8 == 0 && c % 8 == 0 && r < 65536 && c < INT32_MAX,
                 "newton_schulz: need 0 < r <= c, both multiples of 8 (r=%lld c=%lld)",
                 (long long)r, (long long)c);
@@ -1074,28 +1132,44 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
   auto mat_sq = [&](int slot) { return Mat{ws + (size_t)slot * batch * sq, r, sq}; };
   Mat X{x, c, rc}, XT{xt, r, rc};
   double coef[5][3];
+  // Left multiplication by an r x r matrix L of the current iterate: reads X
+  // itself ([k, n] operand) or its transpose.
+  auto left_times = [&](Mat L, Mat x_cur, Mat xt_cur) {
+    Problem p = product(elem, batch, R, C, R, L, direct ? x_cur : xt_cur);
+    p.g.b_kn = direct;
+    return p;
+  };
 
   if (kind == kGram && c_real > r_real) {
     gram_coefficients(coef);
     Mat G = mat_sq(0), G2 = mat_sq(1), Z = mat_sq(2), Q = mat_sq(3), Q2 = mat_sq(4),
         RZ = mat_sq(5);
-    Mat XT2{ws + (size_t)6 * batch * sq, r, rc};
+    // The last workspace slot holds the restarted iterate's transpose, or the
+    // restarted iterate itself when the products read X directly.
+    Mat XT2{ws + (size_t)6 * batch * sq, r, rc}, X2{ws + (size_t)6 * batch * sq, c, rc};
     // G = X X^T
     Problem p = product(elem, batch, R, R, C, X, X);
     set_out(p, G);
     make_symmetric(p);
     prog.push_back(p);
-    Mat xt_cur = XT;
+    Mat x_cur = X, xt_cur = XT;
     for (int i = 0; i < 5; ++i) {
       const float a = (float)coef[i][0], bb = (float)coef[i][1], cc = (float)coef[i][2];
       if (i == 2) {
-        // Restart: X = Q X (in place on X; its transpose goes to XT2), G = X X^T.
-        p = product(elem, batch, R, C, R, Q, xt_cur);
-        set_out(p, X);
-        set_out_t(p, XT2);
+        // Restart: X = Q X, G = X X^T. Read directly, X may not be overwritten
+        // while other tiles still read it: the result goes to X2. Otherwise it
+        // goes in place to X (the product reads X^T) and its transpose to XT2.
+        p = left_times(Q, x_cur, xt_cur);
+        if (direct) {
+          set_out(p, X2);
+          x_cur = X2;
+        } else {
+          set_out(p, X);
+          set_out_t(p, XT2);
+          xt_cur = XT2;
+        }
         prog.push_back(p);
-        xt_cur = XT2;
-        p = product(elem, batch, R, R, C, X, X);
+        p = product(elem, batch, R, R, C, x_cur, x_cur);
         set_out(p, G);
         make_symmetric(p);
         prog.push_back(p);
@@ -1135,7 +1209,7 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
       }
     }
     // out = Q X, rounded to fp16 then bf16.
-    p = product(elem, batch, R, C, R, Q, xt_cur);
+    p = left_times(Q, x_cur, xt_cur);
     p.out_mode = kOutBf16ViaF16;
     set_final_out(p, out, out_transposed, out_ld, out_stride, r_real, c_real);
     prog.push_back(p);
@@ -1148,11 +1222,13 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
   else if (kind == kPolarExpress) polar_express_coefficients(coef);
   else keller_coefficients(coef);
   Mat G = mat_sq(0), P = mat_sq(1);
-  Mat XT2{ws + (size_t)2 * batch * sq, r, rc};
-  Mat xt_cur = XT, xt_next = XT2;
+  // The last workspace slot: the iterate's other transpose buffer, or its
+  // other buffer when the products read X directly (X and X2 alternate).
+  Mat XT2{ws + (size_t)2 * batch * sq, r, rc}, X2{ws + (size_t)2 * batch * sq, c, rc};
+  Mat x_cur = X, x_next = X2, xt_cur = XT, xt_next = XT2;
   for (int i = 0; i < 5; ++i) {
     const float a = (float)coef[i][0], bb = (float)coef[i][1], cc = (float)coef[i][2];
-    Problem p = product(elem, batch, R, R, C, X, X);
+    Problem p = product(elem, batch, R, R, C, x_cur, x_cur);
     set_out(p, G);
     make_symmetric(p);
     prog.push_back(p);
@@ -1161,13 +1237,19 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
     set_out(p, P);
     make_symmetric(p);
     prog.push_back(p);
-    p = product(elem, batch, R, C, R, P, xt_cur);
-    set_addend(p, X, 1.f, a);
+    p = left_times(P, x_cur, xt_cur);
+    set_addend(p, x_cur, 1.f, a);
     if (i < 4) {
-      set_out(p, X);  // X is only read as the addend, element by element
-      set_out_t(p, xt_next);
-      prog.push_back(p);
-      std::swap(xt_cur, xt_next);
+      if (direct) {
+        set_out(p, x_next);
+        prog.push_back(p);
+        std::swap(x_cur, x_next);
+      } else {
+        set_out(p, X);  // X is only read as the addend, element by element
+        set_out_t(p, xt_next);
+        prog.push_back(p);
+        std::swap(xt_cur, xt_next);
+      }
     } else {
       if (kind == kGram) p.out_mode = kOutBf16ViaF16;
       set_final_out(p, out, out_transposed, out_ld, out_stride, r_real, c_real);
@@ -1180,7 +1262,8 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
 bool same_structure(const std::vector<Problem>& a, const std::vector<Problem>& b) {
   if (a.size() != b.size()) return false;
   for (size_t i = 0; i < a.size(); ++i)
-    if (a[i].elem != b[i].elem || a[i].out_mode != b[i].out_mode) return false;
+    if (a[i].elem != b[i].elem || a[i].out_mode != b[i].out_mode || a[i].g.b_kn != b[i].g.b_kn)
+      return false;
   return true;
 }
 

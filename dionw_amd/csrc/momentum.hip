@@ -146,7 +146,7 @@ struct PrepArgs {
   float* momentum;        // run momentum [B, rows, cols]
   const int32_t* idx;     // [B, k] selected rows (ascending), nullptr in full mode
   const float* den;       // [B] Frobenius norm + eps of the block's input
-  void* out_r;            // [B, P_pad, J_pad]: row p of the input, W orientation
+  void* out_r;            // [B, P_pad, J_pad]: row p of the input, W orientation (may be nullptr)
   void* out_t;            // [B, J_pad, P_pad]: its transpose (may be nullptr)
   int64_t rows, cols, k;  // block rows, cols, selected rows
   int64_t p_pad, j_pad;   // padded extents (zeros written in the padding)
@@ -233,12 +233,12 @@ __global__ __launch_bounds__(256) void prepare_kernel(PrepArgs a) {
       vals[i][c] = (T)x;  // padding rows/cols hold u = 0 -> 0
     }
   }
-  // Row-major output [P_pad, J_pad].
-  T* out_r = reinterpret_cast<T*>(a.out_r) + b * a.p_pad * a.j_pad;
+  // Row-major output [P_pad, J_pad] (may be skipped).
+  T* out_r = a.out_r ? reinterpret_cast<T*>(a.out_r) + b * a.p_pad * a.j_pad : nullptr;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t p = p_base + ty + 16 * i;
-    if (p < a.p_pad) {
+    if (out_r && p < a.p_pad) {
       if (j0 + 3 < a.j_pad) {
         typedef T t4 __attribute__((ext_vector_type(4)));
         t4 v = {vals[i][0], vals[i][1], vals[i][2], vals[i][3]};
@@ -401,7 +401,8 @@ int dionw_prepare_ns_input(const float* const* grads, int32_t count, float* mome
                            int32_t nesterov, int32_t write_m, int32_t elem, void* out_rowmajor,
                            void* out_transposed, hipStream_t stream) {
   const bool full = idx == nullptr;
-  DIONW_REQUIRE(den && out_rowmajor, "prepare_ns_input: null pointer");
+  DIONW_REQUIRE(den && (out_rowmajor || out_transposed), "prepare_ns_input: null pointer");
+  DIONW_REQUIRE(out_rowmajor || elem != kF32, "prepare_ns_input: fp32 output needs out_rowmajor");
   DIONW_REQUIRE(momentum || (idx == nullptr && !write_m),
                 "prepare_ns_input: only every-row mode without momentum writes may omit momentum");
   DIONW_REQUIRE(blocks >= 0 && rows > 0 && cols > 0 && k > 0 && k <= rows,
@@ -439,7 +440,8 @@ int dionw_prepare_ns_input(const float* const* grads, int32_t count, float* mome
     a.momentum = momentum ? momentum + b0 * rows * cols : nullptr;
     a.idx = idx;
     a.den = den + b0;
-    a.out_r = static_cast<char*>(out_rowmajor) + b0 * out_elems * out_size;
+    a.out_r = out_rowmajor ? static_cast<char*>(out_rowmajor) + b0 * out_elems * out_size
+                           : nullptr;
     a.out_t = out_transposed ? static_cast<char*>(out_transposed) + b0 * out_elems * out_size
                              : nullptr;
     a.rows = rows;

@@ -52,6 +52,40 @@ def _round8(n: int) -> int:
     return (n + 7) // 8 * 8
 
 
+def prepared_orientations(rows: int, cols: int) -> tuple[bool, bool]:
+    """Which prepared inputs the iteration on ``[rows, cols]`` blocks reads:
+    (weight orientation, its transpose).
+
+    The iterate is the wide orientation (the transpose of a tall block). The
+    library reads the iterate's transpose only when the short side, rounded up
+    to 8, is not a multiple of 32; otherwise its left products take the iterate
+    itself as a ``[k, n]`` operand (``dionw_newton_schulz``).
+    """
+    tall = rows > cols
+    other = _round8(min(rows, cols)) % 32 != 0
+    return (other, True) if tall else (True, other)
+
+
+def prepared_inputs(
+    ortho: HipOrthogonalize, device: torch.device, blocks: int, rows: int, cols: int,
+    name_xr: str, name_xt: str,
+) -> tuple[Tensor | None, Tensor | None]:
+    """Scratch buffers for the prepared inputs of ``[blocks, rows, cols]``: the
+    weight orientation ``[blocks, round8(rows), round8(cols)]`` and its
+    transpose, each None when the iteration does not read it."""
+    p_pad, j_pad = _round8(rows), _round8(cols)
+    want_xr, want_xt = prepared_orientations(rows, cols)
+    xr = (_workspace.buffer(device, name_xr, (blocks, p_pad, j_pad), ortho.dtype)
+          if want_xr else None)
+    xt = (_workspace.buffer(device, name_xt, (blocks, j_pad, p_pad), ortho.dtype)
+          if want_xt else None)
+    return xr, xt
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
 @dataclass(frozen=True)
 class HipOrthogonalize:
     """One Newton-Schulz kind on the HIP kernels.
@@ -100,12 +134,10 @@ class HipOrthogonalize:
                   rowsq.data_ptr(), stream)
         _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, self.norm_safety,
                   float(epsilon), den.data_ptr(), stream)
-        p_pad, j_pad = _round8(rows), _round8(cols)
-        xr = _workspace.buffer(device, "ortho_xr", (blocks, p_pad, j_pad), self.dtype)
-        xt = _workspace.buffer(device, "ortho_xt", (blocks, j_pad, p_pad), self.dtype)
+        xr, xt = prepared_inputs(self, device, blocks, rows, cols, "ortho_xr", "ortho_xt")
         _lib.call("dionw_prepare_ns_input", grads, 1, None, None, den.data_ptr(), blocks, rows,
-                  cols, rows, p_pad, j_pad, 0.0, 0, 0, self.elem, xr.data_ptr(), xt.data_ptr(),
-                  stream)
+                  cols, rows, _round8(rows), _round8(cols), 0.0, 0, 0, self.elem, _ptr(xr),
+                  _ptr(xt), stream)
         run_newton_schulz(self, blocks, rows, cols, xr, xt, out, stream)
         return out if matrix.ndim == 3 else out[0]
 
@@ -135,8 +167,8 @@ def newton_schulz_call(
     blocks: int,
     rows: int,
     cols: int,
-    xr: Tensor,
-    xt: Tensor,
+    xr: Tensor | None,
+    xt: Tensor | None,
     out: Tensor,
     workspace_name: str = "ns_workspace",
 ) -> NewtonSchulzCall:
@@ -144,22 +176,30 @@ def newton_schulz_call(
 
     ``xr`` is the normalized input in the weight's orientation ([blocks,
     round8(rows), round8(cols)]) and ``xt`` its transpose; a tall block
-    (rows > cols) iterates on the transpose. Both are overwritten. The
-    iteration's workspace is the named scratch buffer ``workspace_name``. The
-    result holds device addresses only: ``xr``, ``xt`` and ``out`` must stay
-    alive until the call has been issued.
+    (rows > cols) iterates on the transpose. Either may be None where
+    ``prepared_orientations`` says the iteration does not read it; the others
+    are overwritten. The iteration's workspace is the named scratch buffer
+    ``workspace_name``. The result holds device addresses only: ``xr``, ``xt``
+    and ``out`` must stay alive until the call has been issued.
+
+    Raises:
+        ValueError: If an input the iteration reads is None.
     """
     tall = rows > cols
     if tall:
         x, x_t, r, c, r_real, c_real = xt, xr, _round8(cols), _round8(rows), cols, rows
     else:
         x, x_t, r, c, r_real, c_real = xr, xt, _round8(rows), _round8(cols), rows, cols
+    if x is None or (x_t is None and r % 32 != 0):
+        raise ValueError(f"newton_schulz_call: [{rows}, {cols}] blocks need the prepared "
+                         f"inputs {prepared_orientations(rows, cols)} (weight orientation, "
+                         "transpose)")
     lib = _lib.library()
     need = int(lib.dionw_newton_schulz_workspace(ortho.lib_kind, blocks, r, c))
     ws = _workspace.buffer(out.device, workspace_name, (need,), torch.uint8)
-    return NewtonSchulzCall(ortho.lib_kind, blocks, r, c, x.data_ptr(), x_t.data_ptr(), r_real,
-                            c_real, out.data_ptr(), int(tall), cols, rows * cols, ws.data_ptr(),
-                            need)
+    return NewtonSchulzCall(ortho.lib_kind, blocks, r, c, x.data_ptr(),
+                            0 if x_t is None else x_t.data_ptr(), r_real, c_real,
+                            out.data_ptr(), int(tall), cols, rows * cols, ws.data_ptr(), need)
 
 
 def run_newton_schulz(
@@ -167,8 +207,8 @@ def run_newton_schulz(
     blocks: int,
     rows: int,
     cols: int,
-    xr: Tensor,
-    xt: Tensor,
+    xr: Tensor | None,
+    xt: Tensor | None,
     out: Tensor,
     stream: int,
 ) -> None:

@@ -83,11 +83,13 @@ int dionw_select_rows(const float* scores, const float* row_sumsq, int64_t block
  * (_matrix_step.py:176-179). Every-row mode (idx == NULL, grads given):
  * M = mu (M + G), U = M + G or, with nesterov, G + mu (M + G).
  * Then X = U / den[b] rounded to float16 (elem 0), or bf16(bf16(U) / den)
- * (elem 1, the Keller / Polar Express input), written as [blocks, p_pad,
- * j_pad] (row p = selected row p) and, if out_transposed != NULL, its
- * transpose [blocks, j_pad, p_pad], zeros in the padding. In every-row mode
- * momentum may be NULL with write_m == 0 (U = G). elem 2 writes the
- * raw float32 U as [blocks, k, cols] for a user-supplied orthogonalization.
+ * (elem 1, the Keller / Polar Express input), written, if out_rowmajor !=
+ * NULL, as [blocks, p_pad, j_pad] (row p = selected row p) and, if
+ * out_transposed != NULL, as its transpose [blocks, j_pad, p_pad], zeros in
+ * the padding; at least one must be given. In every-row mode momentum may be
+ * NULL with write_m == 0 (U = G). elem 2 writes the raw float32 U as
+ * [blocks, k, cols] (out_rowmajor required) for a user-supplied
+ * orthogonalization.
  * Replaces the prologue of gram_polar_express (_gram.py:83-87) and the
  * normalization of quintic_triton (_polar_express.py:89-92).
  */
@@ -126,7 +128,9 @@ size_t dionw_newton_schulz_workspace(int32_t kind, int64_t batch, int64_t r, int
  *   kind 1 (POLAR_EXPRESS) / 2 (KELLER): the bf16 quintic (_polar_express.py:
  *     74-104; _keller.py:20-34).
  *   x [batch, r, c] and xt [batch, c, r] (the input and its transpose, both
- *   overwritten), r <= c multiples of 8. The real r_real x c_real region of
+ *   overwritten), r <= c multiples of 8. With r a multiple of 32 the products
+ *   read x itself where they multiply it from the left: xt is then neither
+ *   read nor written and may be NULL. The real r_real x c_real region of
  *   the result goes to out (bf16) with leading dimension out_ld and batch
  *   stride out_stride, transposed when out_transposed (tall blocks).
  */

@@ -35,6 +35,7 @@ from dionw_amd import (
 from dionw_amd.newton_schulz import (
     newton_schulz_call,
     newton_schulz_fn,
+    prepared_orientations,
     run_newton_schulz,
     run_newton_schulz_group,
 )
@@ -83,7 +84,11 @@ def test_group_call_equals_separate_calls(runs) -> None:
         separate.append(out)
         out2 = torch.empty_like(out)
         # A call holds addresses only: its buffers must outlive the grouped launch.
-        xr_d, xt_d = xr.to(DEV), xt.to(DEV)
+        # The grouped leg passes only the inputs the iteration reads, the separate
+        # leg both (an unread transpose is ignored).
+        want_xr, want_xt = prepared_orientations(rows, cols)
+        xr_d = xr.to(DEV) if want_xr else None
+        xt_d = xt.to(DEV) if want_xt else None
         inputs.append((xr_d, xt_d))
         calls.append(newton_schulz_call(ortho, blocks, rows, cols, xr_d, xt_d, out2,
                                         f"test_group_ws#{i}"))

@@ -58,6 +58,42 @@ def test_grouped_newton_schulz_rejects_overlapping_workspaces() -> None:
                   arr(ctypes.c_size_t, 0, 0), None)
 
 
+def test_prepared_orientations() -> None:
+    """The iterate is the wide orientation; its transpose is prepared only when
+    the short side, rounded up to 8, is not a multiple of 32."""
+    from dionw_amd.newton_schulz import prepared_orientations
+
+    assert prepared_orientations(256, 1024) == (True, False)
+    assert prepared_orientations(1024, 256) == (False, True)  # tall: iterates on the transpose
+    assert prepared_orientations(128, 128) == (True, False)
+    assert prepared_orientations(30, 300) == (True, False)    # round8(30) = 32
+    assert prepared_orientations(300, 30) == (False, True)
+    assert prepared_orientations(100, 200) == (True, True)    # round8(100) = 104
+    assert prepared_orientations(200, 100) == (True, True)
+    assert prepared_orientations(72, 72) == (True, True)
+
+
+def test_newton_schulz_needs_the_transpose_it_reads() -> None:
+    """Where r is not a multiple of 32 the products read X^T: a NULL xt is
+    rejected before any launch (fake addresses, never dereferenced); the host
+    wrapper rejects a missing input the same way."""
+    from dionw_amd.newton_schulz import NewtonSchulz, newton_schulz_call, newton_schulz_fn
+
+    need = int(_lib.library().dionw_newton_schulz_workspace(0, 1, 104, 200))
+    fake = 1 << 40
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.call("dionw_newton_schulz", 0, 1, 104, 200, fake, None, 100, 200, fake, 0, 200,
+                  100 * 200, fake + 2**30, need, None)
+    ortho = newton_schulz_fn(NewtonSchulz.GRAM)
+    out = torch.empty(1, 100, 200, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="prepared"):
+        newton_schulz_call(ortho, 1, 100, 200, torch.empty(1, 104, 200, dtype=torch.half), None,
+                           out)
+    with pytest.raises(ValueError, match="prepared"):  # tall: the iterate is the transpose
+        newton_schulz_call(ortho, 1, 1024, 256, torch.empty(1, 1024, 256, dtype=torch.half),
+                           None, torch.empty(1, 1024, 256, dtype=torch.bfloat16))
+
+
 def _planned_launches(runs: list[tuple[int, int, int, int]]) -> int:
     """dionw_newton_schulz_group_launches for (kind, blocks, rows, cols) runs (wide)."""
     n = len(runs)

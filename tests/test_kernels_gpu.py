@@ -150,7 +150,10 @@ def _check_symmetric(dtype: torch.dtype, shape: tuple[int, ...]) -> None:
     assert torch.equal(poly.cpu(), poly.cpu().mT)
 
 
-NS_SHAPES = [(3, 64, 256), (3, 256, 64), (3, 128, 128), (2, 96, 160), (4, 256, 1024), (1, 352, 2048)]
+# Short sides that are multiples of 32 read the iterate directly in the left
+# products; the others (40, 72, 104) read its transpose. Ragged ones pad.
+NS_SHAPES = [(3, 64, 256), (3, 256, 64), (3, 128, 128), (2, 96, 160), (4, 256, 1024), (1, 352, 2048),
+             (2, 30, 300), (2, 300, 30), (2, 40, 200), (2, 200, 40), (1, 72, 72), (2, 100, 520)]
 
 
 @pytest.mark.parametrize("shape", NS_SHAPES)
