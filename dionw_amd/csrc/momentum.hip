@@ -6,8 +6,9 @@
 //               writes (first pass of the every-row path, _momentum_kernels.py:58-77).
 //  block denom  per block: sqrt(sum of the rows' sums of squares) + eps.
 //  prepare      the single pass that writes the decayed momentum and the
-//               normalized 16-bit Newton-Schulz input in both orientations
-//               (_matrix_step.py:172-178 and _gram.py:83-87 fused).
+//               normalized 16-bit Newton-Schulz input in the orientations the
+//               iteration reads (_matrix_step.py:172-178 and _gram.py:83-87
+//               fused), in 64 x 64 tiles (through LDS for the transpose).
 //
 // Row reductions use one 256-thread workgroup per row (its four waves sweep
 // 4 KiB of each stream per step: 8% more HBM throughput than a wave per row at

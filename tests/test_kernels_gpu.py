@@ -96,6 +96,75 @@ def test_accumulate_copy_decay(nesterov: bool) -> None:
     assert torch.equal(out.cpu(), expected_out), "Newton-Schulz input not bit-exact"
 
 
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+@pytest.mark.parametrize("elem", [0, 1], ids=["f16", "bf16"])
+@pytest.mark.parametrize(("mode", "blocks", "rows", "cols", "k"), [
+    ("selected", 3, 40, 4096, 12),    # float4 rows, padding rows past k
+    ("selected", 2, 64, 1001, 16),    # ragged columns: scalar tail and padding columns
+    ("every", 2, 37, 300, 37),        # every-row heavy ball
+    ("nesterov", 2, 20, 14336, 20),   # wide rows
+    ("every", 3, 9, 44, 9),           # short rows
+])
+def test_prepare_row_major_only(elem: int, mode: str, blocks: int, rows: int, cols: int,
+                                k: int) -> None:
+    """prepare_ns_input with the row-major output alone against the same call
+    with both outputs: momentum and X bit-identical, the transpose exact, and X
+    equal to fp16/bf16(U / den) restated on the CPU (IEEE division, one
+    rounding)."""
+    g = _gen(11)
+    mom = torch.randn(blocks, rows, cols, generator=g)
+    grad = torch.randn(blocks * rows, cols, generator=g)
+    den = torch.rand(blocks, generator=g) * 50 + 1
+    full = mode != "selected"
+    idx = None
+    if not full:
+        idx = torch.stack([torch.randperm(rows, generator=g)[:k].sort().values
+                           for _ in range(blocks)]).to(torch.int32)
+    p_pad, j_pad = _round8(k) + 8, _round8(cols)
+    mu, nesterov = 0.95, int(mode == "nesterov")
+    dtype = torch.float16 if elem == 0 else torch.bfloat16
+    grad_d, den_d = grad.to(DEV), den.to(DEV)
+    idx_d = None if idx is None else idx.to(DEV)
+    outs = []
+    for both in (False, True):
+        mom_d = mom.to(DEV)
+        xr = torch.full((blocks, p_pad, j_pad), 7.0, device=DEV, dtype=dtype)  # padding overwritten
+        xt = torch.empty(blocks, j_pad, p_pad, device=DEV, dtype=dtype) if both else None
+        print(f"prepare {mode} {blocks}x{rows}x{cols} k={k} elem={elem} both={both}", flush=True)
+        _lib.call("dionw_prepare_ns_input", _lib.ptr_array([grad_d]) if full else None,
+                  1 if full else 0, mom_d.data_ptr(), None if idx_d is None else idx_d.data_ptr(),
+                  den_d.data_ptr(), blocks, rows, cols, k, p_pad, j_pad, mu, nesterov, 1, elem,
+                  xr.data_ptr(), None if xt is None else xt.data_ptr(), _lib.stream_handle())
+        torch.cuda.synchronize()
+        outs.append((mom_d.cpu(), xr.cpu(), None if xt is None else xt.cpu()))
+    (m1, x1, _), (m2, x2, t2) = outs
+    assert torch.equal(m1, m2), "decayed momentum differs between the two kernels"
+    assert torch.equal(x1, x2), "row-major input differs between the two kernels"
+    assert torch.equal(t2, x2.mT), "transposed output is not the transpose"
+    # CPU restatement of U and X = U / den rounded once (bf16 input rounded first).
+    if full:
+        s = mom + grad.view(blocks, rows, cols)
+        decayed = s * mu
+        u = grad.view(blocks, rows, cols) + decayed if nesterov else s
+        expected_m = decayed
+    else:
+        sel = torch.stack([mom[b, idx[b].long()] for b in range(blocks)])
+        u = sel
+        expected_m = mom.clone()
+        for b in range(blocks):
+            expected_m[b, idx[b].long()] = sel[b] * mu
+    if elem == 1:
+        u = u.to(torch.bfloat16).float()
+    x = (u / den.view(-1, 1, 1)).to(dtype)
+    expected_x = torch.zeros(blocks, p_pad, j_pad, dtype=dtype)
+    expected_x[:, :k, :cols] = x
+    assert torch.equal(m1, expected_m), "momentum differs from the restatement"
+    assert torch.equal(x1, expected_x), "X differs from the restatement"
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize(("batch", "m", "n", "k"), [(1, 64, 64, 64), (3, 100, 72, 136),
                                                     (2, 256, 512, 1024), (5, 352, 352, 2048),
