@@ -53,6 +53,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "dionw_accumulate_scores": (ctypes.c_int, [_pp, _i32, _i64, _i64, _p, _p, _p, _p]),
     "dionw_full_sumsq": (ctypes.c_int, [_pp, _i32, _i64, _i64, _p, _f32, _i32, _p, _p]),
     "dionw_block_denom": (ctypes.c_int, [_p, _i64, _i64, _f32, _f32, _p, _p]),
+    "dionw_normalize_input": (
+        ctypes.c_int,
+        [_p, _i32, _i64, _i64, _i64, _f32, _f32, _p, _p, _i64, _i64, _i32, _p, _p, _p],
+    ),
     "dionw_select_rows": (
         ctypes.c_int,
         [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _p, _p, _p],

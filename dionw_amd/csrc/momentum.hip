@@ -43,6 +43,20 @@ struct AccArgs {
   int vec;                // float4 path: cols % 4 == 0 and 16-byte aligned rows
 };
 
+// Four consecutive input elements (float4 index c of a row of IN) as floats,
+// streamed. IN is float, or the 16-bit type of an Orthogonalize input
+// (dionw_normalize_input), whose conversion to float is exact.
+template <typename IN>
+__device__ __forceinline__ f32x4 load4_nt(const IN* row, int64_t c) {
+  if constexpr (std::is_same<IN, float>::value) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row) + c);
+  } else {
+    typedef IN in4 __attribute__((ext_vector_type(4)));
+    const in4 v = __builtin_nontemporal_load(reinterpret_cast<const in4*>(row) + c);
+    return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  }
+}
+
 // (s0 + s1) + (s2 + s3) of the four wave sums of a row's workgroup.
 __device__ __forceinline__ float row_sum(float v, float* part) {
   v = wave_sum(v);
@@ -51,21 +65,22 @@ __device__ __forceinline__ float row_sum(float v, float* part) {
   return (part[0] + part[1]) + (part[2] + part[3]);
 }
 
-template <int MODE>
+template <int MODE, typename IN = float>
 __global__ __launch_bounds__(kRowThreads) void accumulate_kernel(AccArgs a) {
+  static_assert(MODE == kFullSumsq || std::is_same<IN, float>::value,
+                "only the sums of squares read 16-bit inputs");
   __shared__ float part[2][4];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;  // the grid has exactly one workgroup per row
   const int tensor = (int)(row / a.rows_per_tensor);
   const int64_t local = row - (int64_t)tensor * a.rows_per_tensor;
-  const float* g = a.t.grad[tensor] + local * a.cols;
+  const IN* g = reinterpret_cast<const IN*>(a.t.grad[tensor]) + local * a.cols;
   float* m = a.momentum ? a.momentum + row * a.cols : nullptr;
 
   f32x4 l1 = {0.f, 0.f, 0.f, 0.f};
   f32x4 sq = {0.f, 0.f, 0.f, 0.f};
   if (a.vec) {
     const int64_t n4 = a.cols >> 2;
-    const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
     f32x4* m4 = reinterpret_cast<f32x4*>(m);
     const bool has_m = MODE == kScores || a.momentum;
     // M is read once and written once: streaming (non-temporal) loads and
@@ -94,18 +109,18 @@ __global__ __launch_bounds__(kRowThreads) void accumulate_kernel(AccArgs a) {
       f32x4 gv[kUnroll], mv[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        gv[u] = __builtin_nontemporal_load(g4 + c + u * kRowThreads);
+        gv[u] = load4_nt(g, c + u * kRowThreads);
         mv[u] = load_m(c + u * kRowThreads);
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) step(c + u * kRowThreads, gv[u], mv[u]);
     }
     for (; c < n4; c += kRowThreads)
-      step(c, __builtin_nontemporal_load(g4 + c), load_m(c));
+      step(c, load4_nt(g, c), load_m(c));
   } else {
     // Scalar path (any cols, any alignment): component 0 carries the sums.
     for (int64_t c = tid; c < a.cols; c += kRowThreads) {
-      float gv = g[c];
+      float gv = (float)g[c];
       float s = ((MODE == kScores || a.momentum) ? m[c] : 0.f) + gv;
       if (MODE == kScores) {
         m[c] = s;
@@ -162,7 +177,7 @@ struct PrepArgs {
 
 constexpr int kTile = 64;
 
-template <int ELEM>
+template <int ELEM, typename IN = float>
 __global__ __launch_bounds__(256) void prepare_kernel(PrepArgs a) {
   using T = typename std::conditional<ELEM == kF16, _Float16, __bf16>::type;
   __shared__ T tile[kTile][kTile + 8];
@@ -181,17 +196,17 @@ __global__ __launch_bounds__(256) void prepare_kernel(PrepArgs a) {
     if (p < a.k) {
       const int64_t src_row = a.full ? p : (int64_t)a.idx[b * a.k + p];
       float* m = a.momentum ? a.momentum + (b * a.rows + src_row) * a.cols : nullptr;
-      const float* g = nullptr;
+      const IN* g = nullptr;
       if (a.full) {
         const int64_t tensor = b / a.blocks_per_tensor;
         const int64_t local_row = (b - tensor * a.blocks_per_tensor) * a.rows + p;
-        g = a.t.grad[tensor] + local_row * a.cols;
+        g = reinterpret_cast<const IN*>(a.t.grad[tensor]) + local_row * a.cols;
       }
       if (a.vec && j0 + 3 < a.cols) {
         f32x4 mv = m ? *reinterpret_cast<const f32x4*>(m + j0) : f32x4{0.f, 0.f, 0.f, 0.f};
         f32x4 uv, nm;
         if (a.full) {
-          f32x4 gv = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g + j0));
+          f32x4 gv = load4_nt(g + j0, 0);
           f32x4 s = mv + gv;
           nm = s * a.mu;
           uv = a.nesterov ? gv + nm : s;
@@ -208,7 +223,7 @@ __global__ __launch_bounds__(256) void prepare_kernel(PrepArgs a) {
           if (j < a.cols) {
             float mv = m ? m[j] : 0.f, uv, nm;
             if (a.full) {
-              float gv = g[j];
+              float gv = (float)g[j];
               float s = mv + gv;
               nm = s * a.mu;
               uv = a.nesterov ? gv + nm : s;
@@ -393,6 +408,79 @@ int dionw_block_denom(const float* row_sumsq, int64_t blocks, int64_t rows, floa
   hipLaunchKernelGGL(block_denom_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, row_sumsq,
                      den, rows, safety, eps);
   return check_launch("block_denom");
+}
+
+// See include/dionw_hip.h for the argument contract.
+int dionw_normalize_input(const void* x, int32_t x_elem, int64_t blocks, int64_t rows,
+                          int64_t cols, float safety, float eps, float* row_sumsq, float* den,
+                          int64_t p_pad, int64_t j_pad, int32_t elem, void* out_rowmajor,
+                          void* out_transposed, hipStream_t stream) {
+  DIONW_REQUIRE(x && row_sumsq && den && (out_rowmajor || out_transposed),
+                "normalize_input: null pointer");
+  DIONW_REQUIRE(x_elem == kF16 || x_elem == kBF16 || x_elem == kF32,
+                "normalize_input: bad input type %d", x_elem);
+  DIONW_REQUIRE(elem == kF16 || elem == kBF16, "normalize_input: bad output type %d", elem);
+  DIONW_REQUIRE(blocks >= 0 && rows > 0 && cols > 0, "normalize_input: bad sizes");
+  DIONW_REQUIRE(p_pad >= rows && j_pad >= cols && p_pad % 8 == 0 && j_pad % 8 == 0,
+                "normalize_input: padded extents must cover the block and be multiples of 8");
+  if (blocks == 0) return kOk;
+  DIONW_REQUIRE(blocks <= 65535 && ceil_div(p_pad, kTile) <= 65535 &&
+                    blocks * rows * kRowThreads <= (int64_t)UINT32_MAX,
+                "normalize_input: grid too large");
+  // float4 loads of any input type: rows of a multiple of 4 elements from an
+  // address aligned to 4 elements.
+  const size_t in_size = x_elem == kF32 ? 4 : 2;
+  const bool vec = cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % (4 * in_size) == 0;
+  // Row sums of squares: the every-row pass without momentum (U = x).
+  AccArgs acc{};
+  acc.t.count = 1;
+  acc.t.grad[0] = static_cast<const float*>(x);  // reinterpreted as the input type
+  acc.rowsq = row_sumsq;
+  acc.rows_per_tensor = blocks * rows;
+  acc.cols = cols;
+  acc.vec = vec;
+  const dim3 row_grid((unsigned)(blocks * rows));
+  if (x_elem == kF32)
+    hipLaunchKernelGGL((accumulate_kernel<kFullSumsq, float>), row_grid, dim3(kRowThreads), 0,
+                       stream, acc);
+  else if (x_elem == kF16)
+    hipLaunchKernelGGL((accumulate_kernel<kFullSumsq, _Float16>), row_grid, dim3(kRowThreads), 0,
+                       stream, acc);
+  else
+    hipLaunchKernelGGL((accumulate_kernel<kFullSumsq, __bf16>), row_grid, dim3(kRowThreads), 0,
+                       stream, acc);
+  DIONW_TRY(check_launch("normalize_input"));
+  hipLaunchKernelGGL(block_denom_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, row_sumsq,
+                     den, rows, safety, eps);
+  DIONW_TRY(check_launch("normalize_input"));
+  // X = 16-bit(x / den): the every-row prepare pass without momentum writes.
+  PrepArgs a{};
+  a.t.count = 1;
+  a.t.grad[0] = static_cast<const float*>(x);
+  a.den = den;
+  a.out_r = out_rowmajor;
+  a.out_t = out_transposed;
+  a.rows = rows;
+  a.cols = cols;
+  a.k = rows;
+  a.p_pad = p_pad;
+  a.j_pad = j_pad;
+  a.blocks_per_tensor = blocks;
+  a.full = 1;
+  a.elem = elem;
+  a.vec = vec;
+  const dim3 grid((unsigned)ceil_div(j_pad, kTile), (unsigned)ceil_div(p_pad, kTile),
+                  (unsigned)blocks);
+  if (elem == kF16) {
+    if (x_elem == kF32) hipLaunchKernelGGL((prepare_kernel<kF16, float>), grid, dim3(256), 0, stream, a);
+    else if (x_elem == kF16) hipLaunchKernelGGL((prepare_kernel<kF16, _Float16>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((prepare_kernel<kF16, __bf16>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (x_elem == kF32) hipLaunchKernelGGL((prepare_kernel<kBF16, float>), grid, dim3(256), 0, stream, a);
+    else if (x_elem == kF16) hipLaunchKernelGGL((prepare_kernel<kBF16, _Float16>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((prepare_kernel<kBF16, __bf16>), grid, dim3(256), 0, stream, a);
+  }
+  return check_launch("normalize_input");
 }
 
 // See include/dionw_hip.h for the argument contract.

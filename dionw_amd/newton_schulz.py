@@ -36,6 +36,8 @@ Orthogonalize = Callable[[Tensor, float], Tensor]
 
 # Library kinds (include/dionw_hip.h, dionw_newton_schulz).
 _GRAM, _POLAR_EXPRESS, _KELLER = 0, 1, 2
+# Input types dionw_normalize_input reads as they are.
+_INPUT_ELEMS = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 
 class NewtonSchulz(Enum):
@@ -124,20 +126,18 @@ class HipOrthogonalize:
         out = torch.empty(blocks, rows, cols, device=matrix.device, dtype=torch.bfloat16)
         if blocks == 0:
             return out if matrix.ndim == 3 else out[0]
-        source = batch3.to(torch.float32).contiguous()
+        # float32, float16 and bfloat16 inputs are read as they are (their
+        # conversion to float32 is exact); others are converted first.
+        source = batch3 if batch3.dtype in _INPUT_ELEMS else batch3.to(torch.float32)
+        source = source.contiguous()
         device = source.device
         stream = _lib.stream_handle(device)
         rowsq = _workspace.buffer(device, "ortho_rowsq", (blocks * rows,), torch.float32)
         den = _workspace.buffer(device, "ortho_den", (blocks,), torch.float32)
-        grads = _lib.ptr_array([source])
-        _lib.call("dionw_full_sumsq", grads, 1, blocks * rows, cols, None, 0.0, 0,
-                  rowsq.data_ptr(), stream)
-        _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, self.norm_safety,
-                  float(epsilon), den.data_ptr(), stream)
         xr, xt = prepared_inputs(self, device, blocks, rows, cols, "ortho_xr", "ortho_xt")
-        _lib.call("dionw_prepare_ns_input", grads, 1, None, None, den.data_ptr(), blocks, rows,
-                  cols, rows, _round8(rows), _round8(cols), 0.0, 0, 0, self.elem, _ptr(xr),
-                  _ptr(xt), stream)
+        _lib.call("dionw_normalize_input", source.data_ptr(), _INPUT_ELEMS[source.dtype], blocks,
+                  rows, cols, self.norm_safety, float(epsilon), rowsq.data_ptr(), den.data_ptr(),
+                  _round8(rows), _round8(cols), self.elem, _ptr(xr), _ptr(xt), stream)
         run_newton_schulz(self, blocks, rows, cols, xr, xt, out, stream)
         return out if matrix.ndim == 3 else out[0]
 

@@ -66,6 +66,22 @@ int dionw_block_denom(const float* row_sumsq, int64_t blocks, int64_t rows, floa
                       float eps, float* den, dionw_stream_t stream);
 
 /*
+ * The normalization prologue of the Orthogonalize plugin on a contiguous
+ * [blocks, rows, cols] input x of elem x_elem (0 fp16, 1 bf16, 2 fp32), read
+ * as it is: row sums of squares as dionw_full_sumsq forms them (into
+ * row_sumsq, blocks * rows floats), den as dionw_block_denom, then
+ * X = 16-bit(x / den) of type elem (0 or 1) written as dionw_prepare_ns_input
+ * writes it in every-row mode without momentum (out_rowmajor and/or
+ * out_transposed, padded to p_pad x j_pad). Bit-identical to those three calls
+ * on a float32 copy of x, without the copy. Replaces x.float() and the
+ * division by the norm of _gram.py:85-86 and _polar_express.py:89-92.
+ */
+int dionw_normalize_input(const void* x, int32_t x_elem, int64_t blocks, int64_t rows,
+                          int64_t cols, float safety, float eps, float* row_sumsq, float* den,
+                          int64_t p_pad, int64_t j_pad, int32_t elem, void* out_rowmajor,
+                          void* out_transposed, dionw_stream_t stream);
+
+/*
  * Top-k rows of each block by score: replaces torch.topk(sorted=False) and the
  * index bookkeeping of _selected_update (_matrix_step.py:172-180).
  * Exact: ties at the k-th score take the lowest row indices.

@@ -165,6 +165,61 @@ def test_prepare_row_major_only(elem: int, mode: str, blocks: int, rows: int, co
     assert torch.equal(x1, expected_x), "X differs from the restatement"
 
 
+@pytest.mark.parametrize("x_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("elem", [0, 1], ids=["f16", "bf16"])
+@pytest.mark.parametrize(("blocks", "rows", "cols"), [(3, 64, 256), (2, 37, 300), (2, 9, 1001)])
+def test_normalize_input_reads_16bit_inputs(x_dtype, elem: int, blocks: int, rows: int,
+                                            cols: int) -> None:
+    """dionw_normalize_input on an fp16 / bf16 / fp32 input against
+    full_sumsq + block_denom + prepare_ns_input on its float32 copy (float4 and
+    scalar paths): row sums, denominators and both outputs bit-identical."""
+    g = _gen(12)
+    x = (torch.randn(blocks, rows, cols, generator=g) * 3).to(x_dtype).to(DEV)
+    src = x.float().contiguous()
+    p_pad, j_pad = _round8(rows), _round8(cols)
+    dtype = torch.float16 if elem == 0 else torch.bfloat16
+    st = _lib.stream_handle()
+    results = []
+    for fused in (True, False):
+        rowsq = torch.empty(blocks * rows, device=DEV)
+        den = torch.empty(blocks, device=DEV)
+        xr = torch.full((blocks, p_pad, j_pad), 5.0, device=DEV, dtype=dtype)
+        xt = torch.full((blocks, j_pad, p_pad), 5.0, device=DEV, dtype=dtype)
+        print(f"normalize {x_dtype} {blocks}x{rows}x{cols} elem={elem} fused={fused}", flush=True)
+        if fused:
+            _lib.call("dionw_normalize_input", x.data_ptr(), {torch.float16: 0, torch.bfloat16: 1,
+                      torch.float32: 2}[x_dtype], blocks, rows, cols, 1.02, 1e-7,
+                      rowsq.data_ptr(), den.data_ptr(), p_pad, j_pad, elem, xr.data_ptr(),
+                      xt.data_ptr(), st)
+        else:
+            grads = _lib.ptr_array([src])
+            _lib.call("dionw_full_sumsq", grads, 1, blocks * rows, cols, None, 0.0, 0,
+                      rowsq.data_ptr(), st)
+            _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, 1.02, 1e-7,
+                      den.data_ptr(), st)
+            _lib.call("dionw_prepare_ns_input", grads, 1, None, None, den.data_ptr(), blocks,
+                      rows, cols, rows, p_pad, j_pad, 0.0, 0, 0, elem, xr.data_ptr(),
+                      xt.data_ptr(), st)
+        torch.cuda.synchronize()
+        results.append([t.cpu() for t in (rowsq, den, xr, xt)])
+    for name, a, b in zip(("row sums", "den", "X", "X^T"), *results):
+        assert torch.equal(a, b), f"{name} differs ({x_dtype}, {blocks}x{rows}x{cols})"
+
+
+@pytest.mark.parametrize("kind", [NewtonSchulz.GRAM, NewtonSchulz.POLAR_EXPRESS,
+                                  NewtonSchulz.KELLER])
+@pytest.mark.parametrize("x_dtype", [torch.float16, torch.bfloat16])
+def test_orthogonalize_16bit_input_equals_its_float32_copy(kind, x_dtype) -> None:
+    """A 16-bit input is read as it is; its conversion to float32 is exact, so
+    the result equals that of the float32 copy bit for bit."""
+    g = _gen(13)
+    x = torch.randn(3, 96, 200, generator=g).to(x_dtype).to(DEV)
+    fn = newton_schulz_fn(kind)
+    a, b = fn(x, 1e-7), fn(x.float(), 1e-7)
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu()), f"{kind.value} {x_dtype}"
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize(("batch", "m", "n", "k"), [(1, 64, 64, 64), (3, 100, 72, 136),
                                                     (2, 256, 512, 1024), (5, 352, 352, 2048),
