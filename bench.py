@@ -489,7 +489,7 @@ def main() -> int:
         "phases": phases,
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_nt_pipe_kernel / gemm_nt_kernel (Newton-Schulz products)",
+            "kernel": "gemm_nt_pipe_group_kernel / gemm_nt_pipe_kernel (Newton-Schulz products)",
             "achieved": round(ns_tflops, 1),
             "peak": PEAK_MFMA_TFLOPS,
             "unit": "TFLOP/s",
