@@ -592,6 +592,18 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
   for (int s = 0; s < PSTAGES - 1; ++s)
     if (s < kt_count) issue(s);
   const int lrow = lane & 31, lk = lane >> 5;
+  // A wave computes nothing when no element of its block is ever stored: in a
+  // diagonal tile of a symmetric product, a block wholly below the diagonal
+  // (wm > wn; the epilogue overwrites that part with the mirror of the upper
+  // one), and a block wholly past the stored rows or columns (the padding of a
+  // ragged side). Under the board's power limit the MFMAs saved buy clock for
+  // the rest. The wave still issues its share of the stage loads and takes
+  // every barrier. 16-wave tiles only: in the 4-wave 128x128 kernel the branch
+  // costs more registers and time (+3% on 1408-row products) than it saves.
+  const bool diag_tile = g.sym && tm == tn;
+  const bool idle = CFG::WM * CFG::WN == 16 &&
+                    ((diag_tile && wm > wn) || m0 + wm * WTM >= g.m_lim ||
+                     n0 + wn * WTN >= g.n_lim);
   for (int kt = 0; kt < kt_count; ++kt) {
     const int ahead = min(PSTAGES - 2, kt_count - 1 - kt);  // stages issued after kt
     static_assert(PSTAGES >= 2 && PSTAGES <= 4, "waits cover 0..2 stages ahead");
@@ -601,6 +613,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     if (kt + PSTAGES - 1 < kt_count) issue(kt + PSTAGES - 1);
+    if (idle) continue;
     const T* As = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
     const T* Bs = As + PBM * SBK;
     // Fragments of k-step ks + 1 are read while the MFMAs of k-step ks run.
@@ -645,7 +658,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
   }
 
   staged_epilogue<T, OUT_T, MODE, CFG::threads, PBM, PBN, FM, FN>(
-      g, acc, bidx, m0, n0, wm * WTM, wn * WTN, g.sym && tm == tn, smem);
+      g, acc, bidx, m0, n0, wm * WTM, wn * WTN, diag_tile, smem);
 }
 
 // XCD-aware order: the hardware deals workgroup b to XCD b % 8; each XCD gets a
