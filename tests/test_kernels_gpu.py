@@ -258,6 +258,31 @@ def test_symmetric_products_pipelined(dtype: torch.dtype) -> None:
     _check_symmetric(dtype, (48, 1000, 1024))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_idle_waves_change_no_stored_element(dtype: torch.dtype) -> None:
+    """The 256x256 kernel's waves skip their MFMAs where nothing they compute is
+    stored: below the diagonal of a diagonal tile, and past a ragged side. The
+    symmetric product of a symmetric matrix equals the full product bit for bit
+    (1152 rows: 4.5 tiles), and a product with 1408 rows and 1920 columns equals
+    the same rows and columns of its zero-padded 1536 x 2048 twin."""
+    g = _gen(5)
+    x = (torch.randn(48, 1152, 1152, generator=g) / 34).to(dtype)
+    s = (x + x.mT).to(DEV)
+    sym = _kernels.gemm_nt(s, s, d=s, alpha=0.5, beta=-1.5, symmetric=True)
+    full = _kernels.gemm_nt(s, s, d=s, alpha=0.5, beta=-1.5, symmetric=False)
+    torch.cuda.synchronize()
+    assert torch.equal(sym, full), f"symmetric vs full product, 48 x 1152^2 {dtype}"
+    a = (torch.randn(16, 1408, 1408, generator=g) / 38).to(dtype)
+    b = (torch.randn(16, 1920, 1408, generator=g) / 38).to(dtype)
+    a_pad = torch.zeros(16, 1536, 1408, dtype=dtype)
+    b_pad = torch.zeros(16, 2048, 1408, dtype=dtype)
+    a_pad[:, :1408], b_pad[:, :1920] = a, b
+    ragged = _kernels.gemm_nt(a.to(DEV), b.to(DEV))
+    padded = _kernels.gemm_nt(a_pad.to(DEV), b_pad.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(ragged, padded[:, :1408, :1920]), f"ragged 1408 x 1920 product {dtype}"
+
+
 def _check_symmetric(dtype: torch.dtype, shape: tuple[int, ...]) -> None:
     g = _gen(4)
     x = (torch.randn(*shape, generator=g) / shape[-1] ** 0.5).to(dtype)
