@@ -598,13 +598,13 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
   // one), and a block wholly past the stored rows or columns (the padding of a
   // ragged side). Under the board's power limit the MFMAs saved buy clock for
   // the rest. The wave still issues its share of the stage loads and takes
-  // every barrier. 16-wave tiles only: in the 4-wave 128x128 kernel the branch
-  // costs more registers and time (+3% on 1408-row products) than it saves.
+  // every barrier, in a loop of its own (a branch inside the main loop costs the
+  // 4-wave 128x128 kernel registers and time).
   const bool diag_tile = g.sym && tm == tn;
-  const bool idle = CFG::WM * CFG::WN == 16 &&
-                    ((diag_tile && wm > wn) || m0 + wm * WTM >= g.m_lim ||
-                     n0 + wn * WTN >= g.n_lim);
-  for (int kt = 0; kt < kt_count; ++kt) {
+  const bool idle = (diag_tile && wm > wn) || m0 + wm * WTM >= g.m_lim ||
+                    n0 + wn * WTN >= g.n_lim;
+  // Stage kt has landed for every wave; the stage PSTAGES - 1 ahead is issued.
+  auto advance = [&](int kt) {
     const int ahead = min(PSTAGES - 2, kt_count - 1 - kt);  // stages issued after kt
     static_assert(PSTAGES >= 2 && PSTAGES <= 4, "waits cover 0..2 stages ahead");
     static_assert(2 * (LA + LB) <= 63, "vmcnt counts to 63");
@@ -613,7 +613,11 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     if (kt + PSTAGES - 1 < kt_count) issue(kt + PSTAGES - 1);
-    if (idle) continue;
+  };
+  if (idle) {
+    for (int kt = 0; kt < kt_count; ++kt) advance(kt);
+  } else for (int kt = 0; kt < kt_count; ++kt) {
+    advance(kt);
     const T* As = lds + (kt % PSTAGES) * PSTAGE_ELEMS;
     const T* Bs = As + PBM * SBK;
     // Fragments of k-step ks + 1 are read while the MFMAs of k-step ks run.
