@@ -84,10 +84,21 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * BK + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
+// The float32 result is rounded once more to the 16-bit output. The empty asm
+// keeps that float32 value: without it the compiler may fold the conversion
+// into the preceding multiply-add (v_fma_mixlo_f16, a single rounding) in some
+// epilogues and not in others, so that the same product could round apart.
 template <typename OUT_T, int MODE>
 __device__ __forceinline__ OUT_T round_out(float v) {
+  asm volatile("" : "+v"(v));
   if (MODE == kOutBf16ViaF16) return (OUT_T)(float)(_Float16)v;
   return (OUT_T)v;
+}
+
+// alpha * acc + beta * d with one fixed rounding sequence (beta * d rounded,
+// then one fused multiply-add), so that every epilogue gives the same bits.
+__device__ __forceinline__ float axpby(float alpha, float acc, float beta, float d) {
+  return __builtin_fmaf(alpha, acc, beta * d);
 }
 
 // Decodes the upper-triangle tile t (0 .. T(T+1)/2 - 1) into (tm, tn), tm <= tn.
@@ -229,8 +240,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmArgs g) {
         for (int e = 0; e < 4; ++e) {
           const int row = row0 + e;
           in[e] = row < g.m_lim && col < g.n_lim;
-          float x = g.alpha * acc[i][j][4 * e4 + e];
-          if (D && in[e]) x += g.beta * (float)D[(int64_t)row * g.ldd + col];
+          const float x = D && in[e] ? axpby(g.alpha, acc[i][j][4 * e4 + e], g.beta,
+                                             (float)D[(int64_t)row * g.ldd + col])
+                                     : g.alpha * acc[i][j][4 * e4 + e];
           v[e] = round_out<OUT_T, MODE>(x);
           if (CD) {
             float y = (float)v[e] + (row == col ? g.diag_shift : 0.f);
@@ -397,7 +409,7 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-          tile[row * ELD + col] = round_out<OUT_T, MODE>(g.alpha * acc[i][j][e] + g.beta * dval[e]);
+          tile[row * ELD + col] = round_out<OUT_T, MODE>(axpby(g.alpha, acc[i][j][e], g.beta, dval[e]));
         }
       }
   } else {
