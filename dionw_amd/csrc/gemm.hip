@@ -49,6 +49,8 @@ struct GemmArgs {
   int ct_vec;           // transposed store may use 8-byte vectors
   int tiles_m, tiles_n;
   int b_kn;             // B given as [k, n] (row-major along n) instead of [n, k]
+  int xcd_group;        // 0: each XCD takes one contiguous range of tiles; G > 0:
+                        // XCD x takes every 8th run of G consecutive tiles
 };
 
 struct Problem {
@@ -677,13 +679,26 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
       g, acc, bidx, m0, n0, wm * WTM, wn * WTN, diag_tile, smem);
 }
 
-// XCD-aware order: the hardware deals workgroup b to XCD b % 8; each XCD gets a
-// contiguous range of the problem's logical tiles, so that its L2 sees reuse.
-// Returns -1 for the b that only pad the grid to a multiple of 8.
-__device__ __forceinline__ int xcd_tile(int b, int total) {
-  const int per = total / 8, extra = total % 8, x = b % 8, i = b / 8;
-  if (i >= per + (x < extra ? 1 : 0)) return -1;
-  return x * per + min(x, extra) + i;
+// XCD-aware order: the hardware deals workgroup b to XCD b % 8, and an XCD's
+// workgroups start in the order of b. With group G == 0 each XCD gets one
+// contiguous range of the problem's logical tiles, so that its L2 sees reuse
+// from one round of tiles to the next. With G > 0 (G = the tiles an XCD runs
+// at once) XCD x takes runs x, x + 8, ... of G consecutive tiles: each round of
+// the 8 XCDs covers 8 G consecutive tiles, so the blocks in flight (and the
+// operand bytes the Infinity Cache must hold) are a few instead of eight; the
+// tiles past the last full 8 G are dealt contiguously. Returns -1 for the b
+// that only pad the grid to a multiple of 8.
+__device__ __forceinline__ int xcd_tile(int b, int total, int group) {
+  const int x = b % 8, i = b / 8;
+  int full = 0;
+  if (group > 0) {
+    full = total / (8 * group) * (8 * group);
+    if (i < full / 8) return ((i / group) * 8 + x) * group + i % group;
+  }
+  const int rest = total - full, i2 = i - full / 8;
+  const int per = rest / 8, extra = rest % 8;
+  if (i2 >= per + (x < extra ? 1 : 0)) return -1;
+  return full + x * per + min(x, extra) + i2;
 }
 
 __device__ __forceinline__ int tile_count(const GemmArgs& g) {
@@ -692,7 +707,8 @@ __device__ __forceinline__ int tile_count(const GemmArgs& g) {
 
 template <typename T, typename OUT_T, int MODE, typename CFG, bool BKN>
 __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_kernel(GemmArgs g, int batch) {
-  pipe_tile<T, OUT_T, MODE, CFG, BKN>(g, xcd_tile((int)blockIdx.x, tile_count(g) * batch));
+  pipe_tile<T, OUT_T, MODE, CFG, BKN>(g, xcd_tile((int)blockIdx.x, tile_count(g) * batch,
+                                                  g.xcd_group));
 }
 
 // Several independent products in one launch (the same product of several
@@ -713,7 +729,8 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_group_kernel(Gem
   for (int j = 1; j < grp.count; ++j)
     if ((int)blockIdx.x >= grp.start[j]) q = j;
   const GemmArgs& g = grp.g[q];
-  const int w = xcd_tile((int)blockIdx.x - grp.start[q], tile_count(g) * grp.batch[q]);
+  const int w = xcd_tile((int)blockIdx.x - grp.start[q], tile_count(g) * grp.batch[q],
+                        g.xcd_group);
   if (w < 0) return;  // the whole workgroup: w depends on blockIdx only
   pipe_tile<T, OUT_T, MODE, CFG, BKN>(g, w);
 }
@@ -786,6 +803,12 @@ int64_t pipe_args(const Problem& p, GemmArgs& g) {
     set_error("gemm: grid too large");
     return -1;
   }
+  // Blocks of many 256x256 tiles are dealt in runs of 32 (one tile per CU of
+  // an XCD): measured on Llama-3-8B, -1.7% of product time against contiguous
+  // ranges; blocks of fewer tiles (whose operands stay in cache across an
+  // XCD's rounds) and the 128x128 kernel keep contiguous ranges, where the
+  // runs of 32 or 64 measured 1-1.5% slower (MoE runs).
+  g.xcd_group = CFG::BM == 256 && tiles >= 64 ? 32 : 0;
   return tiles * p.batch;
 }
 
