@@ -804,7 +804,7 @@ int64_t pipe_args(const Problem& p, GemmArgs& g) {
     return -1;
   }
   // Blocks of many 256x256 tiles are dealt in runs of 32 (one tile per CU of
-  // an XCD): measured on Llama-3-8B, -1.7% of product time against contiguous
+  // an XCD): measured on Llama-3-8B, -2.6% of product time against contiguous
   // ranges; blocks of fewer tiles (whose operands stay in cache across an
   // XCD's rounds) and the 128x128 kernel keep contiguous ranges, where the
   // runs of 32 or 64 measured 1-1.5% slower (MoE runs).
