@@ -89,6 +89,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [_p, _i64, _i64, _i64, _i64, _p, _p, _f32, _f32, _p, _p, _p, _p],
     ),
+    "dionw_normuon_stats_noalloc": (
+        ctypes.c_int,
+        [_p, _i64, _i64, _i64, _i64, _p, _p, _f32, _f32, _p, _p, _p],
+    ),
     "dionw_apply_update": (
         ctypes.c_int,
         [_pp, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _f32, _f32, _i32, _p],

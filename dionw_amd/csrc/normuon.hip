@@ -16,8 +16,18 @@
 
 #include "common.h"
 
+#include <mutex>
+
 namespace dionw {
 namespace {
+
+// Device scratch of dionw_normuon_stats_noalloc: the per-row sums s and
+// s / d^2 (two floats per selected row) that block_scale_kernel reduces.
+// Every element it reads is written first by row_stats_kernel in the same
+// call, so nothing needs clearing between calls. One copy per GPU, held until
+// the process ends; calls that overlap on one GPU race on it.
+constexpr int64_t kNoAllocRows = int64_t(1) << 19;  // 524288 selected rows, 4 MiB
+static __device__ __align__(256) float scratch[2 * kNoAllocRows];
 
 struct StatArgs {
   const __bf16* o;      // [B, k, cols]
@@ -278,18 +288,11 @@ int apply_launch(float* const* params, float* const* shadows, int32_t count,
   return kOk;
 }
 
-}  // namespace
-}  // namespace dionw
-
-using namespace dionw;
-
-extern "C" {
-
-int dionw_normuon_stats(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows,
-                        int64_t cols, const int32_t* idx, float* variance, float beta2,
-                        float step, float* rowd, float* scratch, float* scale,
-                        hipStream_t stream) {
-  DIONW_REQUIRE(orthogonal && variance && rowd && scratch && scale, "normuon_stats: null pointer");
+int stats_launch(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows, int64_t cols,
+                 const int32_t* idx, float* variance, float beta2, float step, float* rowd,
+                 float* partials, float* scale, hipStream_t stream) {
+  DIONW_REQUIRE(orthogonal && variance && rowd && partials && scale,
+                "normuon_stats: null pointer");
   DIONW_REQUIRE(k > 0 && k <= rows && cols > 0, "normuon_stats: bad sizes");
   DIONW_REQUIRE(idx || k == rows, "normuon_stats: every-row mode needs k == rows");
   if (blocks == 0) return kOk;
@@ -298,8 +301,8 @@ int dionw_normuon_stats(const void* orthogonal, int64_t blocks, int64_t k, int64
   a.variance = variance;
   a.idx = idx;
   a.rowd = rowd;
-  a.rows_s = scratch;
-  a.rows_t = scratch + blocks * k;
+  a.rows_s = partials;
+  a.rows_t = partials + blocks * k;
   a.blocks = blocks;
   a.k = k;
   a.rows = rows;
@@ -312,6 +315,74 @@ int dionw_normuon_stats(const void* orthogonal, int64_t blocks, int64_t k, int64
   hipLaunchKernelGGL(block_scale_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, a.rows_s,
                      a.rows_t, scale, k, step);
   return check_launch("normuon_scale");
+}
+
+// The device address of `scratch` on the stream's GPU, looked up once per
+// device with that device current (each GPU holds its own copy at its own
+// address; the array's name in host code is only a stand-in for it).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+float* g_scratch[kMaxDevices] = {};
+
+int device_scratch(hipStream_t stream, float** out) {
+  int current = -1;
+  hipError_t rc = hipGetDevice(&current);
+  if (rc != hipSuccess) {
+    set_error("normuon_stats_noalloc: hipGetDevice failed: %s", hipGetErrorString(rc));
+    return kHipError;
+  }
+  int device = current;
+  if (stream) {
+    rc = hipStreamGetDevice(stream, &device);
+    if (rc != hipSuccess) {
+      set_error("normuon_stats_noalloc: hipStreamGetDevice failed: %s", hipGetErrorString(rc));
+      return kHipError;
+    }
+  }
+  DIONW_REQUIRE(device == current,
+                "normuon_stats_noalloc: the stream is on device %d but device %d is current",
+                device, current);
+  DIONW_REQUIRE(device >= 0 && device < kMaxDevices, "normuon_stats_noalloc: device %d", device);
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (!g_scratch[device]) {
+    void* ptr = nullptr;
+    rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || !ptr) {
+      set_error("normuon_stats_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(rc));
+      return kHipError;
+    }
+    g_scratch[device] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch[device];
+  return kOk;
+}
+
+}  // namespace
+}  // namespace dionw
+
+using namespace dionw;
+
+extern "C" {
+
+int dionw_normuon_stats(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows,
+                        int64_t cols, const int32_t* idx, float* variance, float beta2,
+                        float step, float* rowd, float* partials, float* scale,
+                        hipStream_t stream) {
+  return stats_launch(orthogonal, blocks, k, rows, cols, idx, variance, beta2, step, rowd,
+                      partials, scale, stream);
+}
+
+int dionw_normuon_stats_noalloc(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows,
+                                int64_t cols, const int32_t* idx, float* variance, float beta2,
+                                float step, float* rowd, float* scale, hipStream_t stream) {
+  DIONW_REQUIRE(blocks <= 0 || k <= 0 || (k <= kNoAllocRows && blocks <= kNoAllocRows / k),
+                "normuon_stats_noalloc: %lld blocks x %lld selected rows exceed the %lld rows "
+                "of its device scratch (use dionw_normuon_stats with a caller workspace)",
+                (long long)blocks, (long long)k, (long long)kNoAllocRows);
+  float* partials = nullptr;
+  DIONW_TRY(device_scratch(stream, &partials));
+  return stats_launch(orthogonal, blocks, k, rows, cols, idx, variance, beta2, step, rowd,
+                      partials, scale, stream);
 }
 
 int dionw_apply_update(float* const* params, int32_t count, int64_t blocks_per_tensor,

@@ -200,6 +200,20 @@ int dionw_normuon_stats(const void* orthogonal, int64_t blocks, int64_t k, int64
                         dionw_stream_t stream);
 
 /*
+ * dionw_normuon_stats without the scratch argument: the per-row partial sums
+ * go to a device array inside the library (4 MiB per GPU, held until the
+ * process ends), so the call allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Limit: blocks * k <= 524288 selected rows; larger calls are rejected.
+ * The stream must belong to the current device. Calls that overlap on one GPU
+ * (two streams, two threads) race on the shared array.
+ */
+int dionw_normuon_stats_noalloc(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows,
+                                int64_t cols, const int32_t* idx, float* variance, float beta2,
+                                float step, float* rowd, float* scale, dionw_stream_t stream);
+
+/*
  * The weight update of a run: W *= decay on every row when apply_decay, then
  * W[row] += O[slot] / rowd[slot] * scale[b] on the selected rows (rowd == NULL:
  * W[row] += O[slot] * (scale ? scale[b] : step)). Replaces _apply and
