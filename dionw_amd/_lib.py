@@ -50,16 +50,16 @@ _psize = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "dionw_last_error": (ctypes.c_char_p, []),
     "dionw_abi_version": (ctypes.c_int, []),
-    "dionw_accumulate_scores": (ctypes.c_int, [_pp, _i32, _i64, _i64, _p, _p, _p, _p]),
-    "dionw_full_sumsq": (ctypes.c_int, [_pp, _i32, _i64, _i64, _p, _f32, _i32, _p, _p]),
-    "dionw_block_denom": (ctypes.c_int, [_p, _i64, _i64, _f32, _f32, _p, _p]),
+    "dionw_accumulate_scores": (ctypes.c_int, [_pp, _i32, _i64, _i64, _p, _p, _p, _i32, _p]),
+    "dionw_full_sumsq": (ctypes.c_int, [_pp, _i32, _i64, _i64, _p, _f32, _i32, _p, _i32, _p]),
+    "dionw_block_denom": (ctypes.c_int, [_p, _i64, _i64, _f32, _f32, _p, _i32, _p]),
     "dionw_normalize_input": (
         ctypes.c_int,
         [_p, _i32, _i64, _i64, _i64, _f32, _f32, _p, _p, _i64, _i64, _i32, _p, _p, _p],
     ),
     "dionw_select_rows": (
         ctypes.c_int,
-        [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _p, _p, _p],
+        [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _p, _p, _i32, _p],
     ),
     "dionw_prepare_ns_input": (
         ctypes.c_int,
@@ -72,6 +72,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          _f32, _p, _i64, _i64, _p, _i64, _i64, _i32, _p],
     ),
     "dionw_newton_schulz_workspace": (ctypes.c_size_t, [_i32, _i64, _i64, _i64]),
+    "dionw_ns_coefficients": (ctypes.c_int, [_i32, ctypes.POINTER(ctypes.c_double)]),
     "dionw_newton_schulz": (
         ctypes.c_int,
         [_i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _i32, _i64, _i64, _p,

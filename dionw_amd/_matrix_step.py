@@ -218,6 +218,8 @@ def step_run(
     ortho = bucket.orthogonalize
     fused = isinstance(ortho, HipOrthogonalize)
     safety = ortho.norm_safety if fused else 1.0
+    # The element type of the iteration fixes how its input norm rounds.
+    norm_elem = ortho.elem if fused else _lib.F32
     grads = _lib.ptr_array(run.grads)
     momentum = run.momentum
     queue = ACTIVE_RUNS.get() if fused else None
@@ -234,15 +236,15 @@ def step_run(
         idx = _workspace.buffer(device, "idx" + own, (blocks, k), torch.int32)
         slot = _workspace.buffer(device, "slot" + own, (blocks, rows), torch.int32)
         _lib.call("dionw_accumulate_scores", grads, count, per_param * rows, cols,
-                  momentum.data_ptr(), scores.data_ptr(), rowsq.data_ptr(), stream)
+                  momentum.data_ptr(), scores.data_ptr(), rowsq.data_ptr(), norm_elem, stream)
         _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k,
                   safety, NEWTON_SCHULZ_EPS, idx.data_ptr(), slot.data_ptr(), den.data_ptr(),
-                  stream)
+                  norm_elem, stream)
     elif fused:
         _lib.call("dionw_full_sumsq", grads, count, per_param * rows, cols, momentum.data_ptr(),
-                  mu, int(nesterov), rowsq.data_ptr(), stream)
+                  mu, int(nesterov), rowsq.data_ptr(), norm_elem, stream)
         _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, safety, NEWTON_SCHULZ_EPS,
-                  den.data_ptr(), stream)
+                  den.data_ptr(), norm_elem, stream)
     idx_ptr = None if idx is None else idx.data_ptr()
 
     if fused:

@@ -35,6 +35,6 @@ extern "C" {
 
 const char* dionw_last_error(void) { return dionw::g_last_error.c_str(); }
 
-int dionw_abi_version(void) { return 1; }
+int dionw_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -4,7 +4,12 @@
 // operands row-major along k, computed with v_mfma_f32_32x32x16_{f16,bf16}
 // (fp32 accumulation) from LDS-staged k tiles (64 deep; 32 deep where k is an
 // odd multiple of 32). The epilogue forms
-// alpha * acc + beta * D[i,j] and rounds once to the storage type.
+// alpha * acc + beta * D[i,j] and rounds once to the storage type; in mode
+// kOutRoundAcc it rounds the product to the storage type first, then forms
+// alpha * bf16(acc) + beta * D and rounds again (a product stored by one
+// matmul and combined by a separate elementwise op, as the reference's cuBLAS
+// quintic does, _polar_express.py:61-70). Float32 operands run on
+// v_mfma_f32_32x32x2_f32 (gemm_f32_kernel).
 //
 //  symmetric mode  only tiles on and above the diagonal are computed and each
 //                  is stored twice (itself and its mirror): X X^T (syrk,
@@ -31,7 +36,11 @@ namespace {
 
 constexpr int BK = 64;  // k depth of one LDS stage (4 MFMA k-steps of 16)
 
-enum OutMode : int { kOutSame = 0, kOutBf16ViaF16 = 1 };
+// kOutSame: output in the operand type. kOutBf16ViaF16: float16 operands, output
+// rounded to float16 and then to bfloat16 (the Gram iteration's last product,
+// _gram.py:89). kOutRoundAcc: output in the operand type, the product rounded to
+// it before alpha and beta D are applied.
+enum OutMode : int { kOutSame = 0, kOutBf16ViaF16 = 1, kOutRoundAcc = 2 };
 
 struct GemmArgs {
   const void* a;
@@ -101,6 +110,14 @@ __device__ __forceinline__ OUT_T round_out(float v) {
 // then one fused multiply-add), so that every epilogue gives the same bits.
 __device__ __forceinline__ float axpby(float alpha, float acc, float beta, float d) {
   return __builtin_fmaf(alpha, acc, beta * d);
+}
+
+// The product as the epilogue combines it: the float32 accumulator, or in mode
+// kOutRoundAcc the accumulator rounded to the output type.
+template <typename OUT_T, int MODE>
+__device__ __forceinline__ float product_value(float acc) {
+  if constexpr (MODE == kOutRoundAcc) return (float)round_out<OUT_T, kOutSame>(acc);
+  return acc;
 }
 
 // Decodes the upper-triangle tile t (0 .. T(T+1)/2 - 1) into (tm, tn), tm <= tn.
@@ -242,9 +259,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmArgs g) {
         for (int e = 0; e < 4; ++e) {
           const int row = row0 + e;
           in[e] = row < g.m_lim && col < g.n_lim;
-          const float x = D && in[e] ? axpby(g.alpha, acc[i][j][4 * e4 + e], g.beta,
+          const float pv = product_value<OUT_T, MODE>(acc[i][j][4 * e4 + e]);
+          const float x = D && in[e] ? axpby(g.alpha, pv, g.beta,
                                              (float)D[(int64_t)row * g.ldd + col])
-                                     : g.alpha * acc[i][j][4 * e4 + e];
+                                     : g.alpha * pv;
           v[e] = round_out<OUT_T, MODE>(x);
           if (CD) {
             float y = (float)v[e] + (row == col ? g.diag_shift : 0.f);
@@ -285,19 +303,20 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_nt_kernel(GemmArgs g) {
   }
 }
 
-// ---- pipelined large-tile kernel ------------------------------------------------
+// ---- pipelined tile kernels ----------------------------------------------------
 //
-// 256x256 output tile per workgroup of 4 waves (2x2, 128x128 per wave: 16
-// accumulators of 32x32 in AGPRs, one wave per SIMD). k advances 32 at a time
-// through a 4-stage LDS ring filled by direct-to-LDS loads
-// (global_load_lds_dwordx4): a stage is requested three stages before it is
-// consumed, so HBM latency hides behind ~3000 cycles of MFMA work. Waits are
-// explicit: before a stage is read every wave waits for its own loads of it
-// (vmcnt) and for its reads of the stage about to be refilled (lgkmcnt), then
-// the workgroup meets at one barrier. Rows beyond m / n load a clamped valid
-// row (only outputs that are never stored see them), so every wave issues the
-// same number of loads per stage and the vmcnt arithmetic is exact; k must be
-// a multiple of 32.
+// Two tile shapes (PipeCfg): 256x256 per workgroup of 16 waves (4x4, 64x64 per
+// wave: 4 accumulators of 32x32) and 128x128 per workgroup of 4 waves (2x2,
+// 64x64 per wave, two workgroups per CU). k advances through an LDS ring filled
+// by direct-to-LDS loads (global_load_lds_dwordx4): two 64-deep stages when k
+// is a multiple of 64, four 32-deep stages when it is an odd multiple of 32; a
+// stage is requested one stage (64-deep) or three stages (32-deep) before it is
+// consumed. Waits are explicit: before a stage is read every wave waits for its
+// own loads of it (vmcnt) and for its reads of the stage about to be refilled
+// (lgkmcnt), then the workgroup meets at one barrier. Rows beyond m / n load a
+// clamped valid row (only outputs that are never stored see them), so every
+// wave issues the same number of loads per stage and the vmcnt arithmetic is
+// exact; k must be a multiple of 32.
 
 // Tile configuration: BM x BN output tile, WM x WN waves, STAGES-deep LDS ring of
 // BK-deep stages.
@@ -411,7 +430,8 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-          tile[row * ELD + col] = round_out<OUT_T, MODE>(axpby(g.alpha, acc[i][j][e], g.beta, dval[e]));
+          tile[row * ELD + col] = round_out<OUT_T, MODE>(
+              axpby(g.alpha, product_value<OUT_T, MODE>(acc[i][j][e]), g.beta, dval[e]));
         }
       }
   } else {
@@ -423,7 +443,8 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& g, f32x16 (&acc)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int row = wrow0 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-          tile[row * ELD + col] = round_out<OUT_T, MODE>(g.alpha * acc[i][j][e]);
+          tile[row * ELD + col] =
+              round_out<OUT_T, MODE>(g.alpha * product_value<OUT_T, MODE>(acc[i][j][e]));
         }
       }
   }
@@ -735,6 +756,119 @@ __global__ __launch_bounds__(CFG::threads, 1) void gemm_nt_pipe_group_kernel(Gem
   pipe_tile<T, OUT_T, MODE, CFG, BKN>(g, w);
 }
 
+// ---- float32 products -----------------------------------------------------------
+//
+// alpha A B^T + beta D with float32 operands and output on v_mfma_f32_32x32x2_f32:
+// products and sums in float32, as the reference's symmetric kernels compute
+// float32 inputs (tl.dot with "ieee" precision, _symmetric_kernels.py:275, 311).
+// 64x64 output tile per workgroup of 4 waves (one 32x32 fragment each); k moves
+// through 32-deep LDS stages, the next stage held in registers while the current
+// one is multiplied. Any sizes and strides: rows and k past the edge load zeros.
+// Symmetric mode computes the tiles on and above the diagonal and stores each
+// also mirrored (the diagonal tiles' lower halves from their upper ones).
+constexpr int kF32Tile = 64, kF32Depth = 32, kF32Ld = kF32Depth + 1;
+
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t tiles, int vec) {
+  __shared__ float as[2][kF32Tile * kF32Ld];
+  __shared__ float bs[2][kF32Tile * kF32Ld];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t bidx = (int64_t)blockIdx.x / tiles;
+  const int t = (int)((int64_t)blockIdx.x - bidx * tiles);
+  int tm, tn;
+  if (g.sym) {
+    tri_tile(t, tm, tn);
+  } else {
+    tm = t / g.tiles_n;
+    tn = t - tm * g.tiles_n;
+  }
+  const int m0 = tm * kF32Tile, n0 = tn * kF32Tile;
+  const float* A = reinterpret_cast<const float*>(g.a) + bidx * g.sa;
+  const float* B = reinterpret_cast<const float*>(g.b) + bidx * g.sb;
+  // Thread tid stages k columns 4 (tid % 8) .. + 3 of tile rows tid / 8 and
+  // tid / 8 + 32 of each operand.
+  const int lrow = tid >> 3, lk = 4 * (tid & 7);
+  float ra[2][4], rb[2][4];
+  auto fetch = [&](const float* M, int64_t ld, int r0, int lim, int k0, float (&r)[2][4]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = r0 + lrow + 32 * h, kk = k0 + lk;
+      const float* src = M + (int64_t)row * ld + kk;
+      if (row < lim && vec && kk + 3 < g.k) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src);
+        r[h][0] = v.x; r[h][1] = v.y; r[h][2] = v.z; r[h][3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[h][e] = (row < lim && kk + e < g.k) ? src[e] : 0.f;
+      }
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        as[buf][(lrow + 32 * h) * kF32Ld + lk + e] = ra[h][e];
+        bs[buf][(lrow + 32 * h) * kF32Ld + lk + e] = rb[h][e];
+      }
+  };
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  const int stages = (g.k + kF32Depth - 1) / kF32Depth;
+  fetch(A, g.lda, m0, g.m, 0, ra);
+  fetch(B, g.ldb, n0, g.n, 0, rb);
+  stash(0);
+  __syncthreads();
+  const int frow = lane & 31, fk = lane >> 5;
+  for (int st = 0; st < stages; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < stages) {
+      fetch(A, g.lda, m0, g.m, (st + 1) * kF32Depth, ra);
+      fetch(B, g.ldb, n0, g.n, (st + 1) * kF32Depth, rb);
+    }
+    const float* a_t = as[buf] + (wm * 32 + frow) * kF32Ld + fk;
+    const float* b_t = bs[buf] + (wn * 32 + frow) * kF32Ld + fk;
+#pragma unroll
+    for (int ks = 0; ks < kF32Depth / 2; ++ks)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a_t[2 * ks], b_t[2 * ks], acc, 0, 0, 0);
+    if (st + 1 < stages) stash(buf ^ 1);
+    __syncthreads();
+  }
+  // Element e of lane l: row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
+  const float* D = g.d ? reinterpret_cast<const float*>(g.d) + bidx * g.sd : nullptr;
+  float* C = g.c ? reinterpret_cast<float*>(g.c) + bidx * g.sc : nullptr;
+  float* CT = g.ct ? reinterpret_cast<float*>(g.ct) + bidx * g.sct : nullptr;
+  const bool diag_tile = g.sym && tm == tn;
+  const int col = n0 + wn * 32 + frow;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = m0 + wm * 32 + 8 * (e >> 2) + 4 * fk + (e & 3);
+    if (row >= g.m_lim || col >= g.n_lim) continue;
+    const float v = D ? axpby(g.alpha, acc[e], g.beta, D[(int64_t)row * g.ldd + col])
+                      : g.alpha * acc[e];
+    if (C && !(diag_tile && row > col)) C[(int64_t)row * g.ldc + col] = v;
+    if (CT && !(g.sym && row >= col)) CT[(int64_t)col * g.ldct + row] = v;
+  }
+}
+
+int launch_f32(const Problem& p, hipStream_t stream) {
+  GemmArgs g = p.g;
+  g.tiles_m = (g.m + kF32Tile - 1) / kF32Tile;
+  g.tiles_n = (g.n + kF32Tile - 1) / kF32Tile;
+  const int64_t tiles = g.sym ? (int64_t)g.tiles_m * (g.tiles_m + 1) / 2
+                              : (int64_t)g.tiles_m * g.tiles_n;
+  if (tiles * p.batch > INT32_MAX) {
+    set_error("gemm: grid too large");
+    return kInvalid;
+  }
+  const bool vec = g.lda % 4 == 0 && g.ldb % 4 == 0 && g.sa % 4 == 0 && g.sb % 4 == 0 &&
+                   aligned16(g.a) && aligned16(g.b);
+  hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)(tiles * p.batch)), dim3(256), 0, stream, g,
+                     tiles, (int)vec);
+  return check_launch("gemm_f32");
+}
+
 // ---- launch configuration ----------------------------------------------------
 
 
@@ -946,6 +1080,13 @@ bool operands_ok(const GemmArgs& g) {
 int launch(const Problem& p, hipStream_t stream) {
   const GemmArgs& g = p.g;
   if (g.m <= 0 || g.n <= 0 || g.k <= 0 || p.batch <= 0) return kOk;
+  if (p.elem == kF32) {
+    if (g.b_kn) {
+      set_error("gemm: float32 products take B as [n, k]");
+      return kInvalid;
+    }
+    return launch_f32(p, stream);
+  }
   if (!operands_ok(g)) {
     set_error("gemm: k, operand row strides and batch strides must be multiples of 8 "
               "elements and operands 16-byte aligned");
@@ -959,7 +1100,10 @@ int launch(const Problem& p, hipStream_t stream) {
     if (p.out_mode == kOutBf16ViaF16) return launch_typed<_Float16, __bf16, kOutBf16ViaF16>(p, stream);
     return launch_typed<_Float16, _Float16, kOutSame>(p, stream);
   }
-  if (p.elem == kBF16) return launch_typed<__bf16, __bf16, kOutSame>(p, stream);
+  if (p.elem == kBF16) {
+    if (p.out_mode == kOutRoundAcc) return launch_typed<__bf16, __bf16, kOutRoundAcc>(p, stream);
+    return launch_typed<__bf16, __bf16, kOutSame>(p, stream);
+  }
   set_error("gemm: unsupported element type %d", p.elem);
   return kInvalid;
 }
@@ -1012,6 +1156,8 @@ int launch_group(const std::vector<const Problem*>& ps, hipStream_t stream) {
       return launch_pipe_group<_Float16, __bf16, kOutBf16ViaF16>(live, stream);
     return launch_pipe_group<_Float16, _Float16, kOutSame>(live, stream);
   }
+  if (live[0]->out_mode == kOutRoundAcc)
+    return launch_pipe_group<__bf16, __bf16, kOutRoundAcc>(live, stream);
   return launch_pipe_group<__bf16, __bf16, kOutSame>(live, stream);
 }
 
@@ -1103,7 +1249,17 @@ void keller_coefficients(double out[5][3]) {
   }
 }
 
-enum Kind : int { kGram = 0, kPolarExpress = 1, kKeller = 2 };
+// Library kinds: the Gram iteration, the two bf16 quintics with each line's
+// product and elementwise terms rounded once (the symmetric-kernel variants,
+// _polar_express.py:74-104), and the same quintics with the products rounded
+// to bf16 before the elementwise terms (the cuBLAS variants, :43-71).
+enum Kind : int {
+  kGram = 0,
+  kPolarExpress = 1,
+  kKeller = 2,
+  kPolarExpressCublas = 3,
+  kKellerCublas = 4,
+};
 
 size_t elems_needed(int kind, int64_t batch, int64_t r, int64_t c) {
   const bool gram = kind == kGram;  // the Gram iteration needs the most
@@ -1153,6 +1309,18 @@ size_t dionw_newton_schulz_workspace(int32_t kind, int64_t batch, int64_t r, int
   return elems_needed(kind, batch, r, c) * 2;
 }
 
+int dionw_ns_coefficients(int32_t kind, double* out) {
+  DIONW_REQUIRE(out, "ns_coefficients: null output");
+  DIONW_REQUIRE(kind >= kGram && kind <= kKellerCublas, "ns_coefficients: unknown kind %d", kind);
+  double coef[5][3];
+  if (kind == kGram) gram_coefficients(coef);
+  else if (kind == kPolarExpress || kind == kPolarExpressCublas) polar_express_coefficients(coef);
+  else keller_coefficients(coef);
+  for (int i = 0; i < 5; ++i)
+    for (int j = 0; j < 3; ++j) out[3 * i + j] = coef[i][j];
+  return kOk;
+}
+
 }  // extern "C"
 
 namespace dionw {
@@ -1163,8 +1331,7 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
                int64_t r_real, int64_t c_real, void* out, int32_t out_transposed, int64_t out_ld,
                int64_t out_stride, void* workspace, size_t workspace_bytes,
                std::vector<Problem>& prog) {
-  DIONW_REQUIRE(kind == kGram || kind == kPolarExpress || kind == kKeller,
-                "newton_schulz: unknown kind %d", kind);
+  DIONW_REQUIRE(kind >= kGram && kind <= kKellerCublas, "newton_schulz: unknown kind %d", kind);
   // With r a multiple of 32 the products that multiply X from the left read
   // it directly as a [k, n] operand, so xt is neither read nor written.
   const bool direct = r % 32 == 0;
@@ -1269,9 +1436,14 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
   }
 
   // Standard iteration (square Gram blocks, fp16) or the bf16 quintic:
-  // X = a X + (c A A + b A) X with A = X X^T, five times.
+  // X = a X + (c A A + b A) X with A = X X^T, five times. The cuBLAS variants
+  // round A A and P X to bf16 before the elementwise terms: P = b A + c bf16(A A),
+  // X = a X + bf16(P X). A tall block is iterated in its wide orientation: the
+  // reference's right products x^T x and x P of the tall x are the transposes of
+  // X X^T and P X, with the same roundings.
+  const bool cublas = kind == kPolarExpressCublas || kind == kKellerCublas;
   if (kind == kGram) gram_coefficients(coef);
-  else if (kind == kPolarExpress) polar_express_coefficients(coef);
+  else if (kind == kPolarExpress || kind == kPolarExpressCublas) polar_express_coefficients(coef);
   else keller_coefficients(coef);
   Mat G = mat_sq(0), P = mat_sq(1);
   // The last workspace slot: the iterate's other transpose buffer, or its
@@ -1286,11 +1458,13 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
     prog.push_back(p);
     p = product(elem, batch, R, R, R, G, G);
     set_addend(p, G, cc, bb);
+    if (cublas) p.out_mode = kOutRoundAcc;
     set_out(p, P);
     make_symmetric(p);
     prog.push_back(p);
     p = left_times(P, x_cur, xt_cur);
     set_addend(p, x_cur, 1.f, a);
+    if (cublas) p.out_mode = kOutRoundAcc;
     if (i < 4) {
       if (direct) {
         set_out(p, x_next);

@@ -4,7 +4,16 @@
 //               (the selected path; replaces _momentum_kernels.py:40-55).
 //  full sumsq   sum of squares of the Newton-Schulz input U of every row, no
 //               writes (first pass of the every-row path, _momentum_kernels.py:58-77).
-//  block denom  per block: sqrt(sum of the rows' sums of squares) + eps.
+//  block denom  per block: sqrt(sum of the rows' sums of squares) * safety + eps.
+//
+// The sums of squares feed the Frobenius normalization of the Newton-Schulz
+// input. For the float16 Gram iteration they are sums of the float32 values
+// (_gram.py:85-86, the norm of x.float()). The bfloat16 quintics normalize the
+// input rounded to bfloat16 by its norm, itself a bfloat16 tensor
+// (_polar_express.py:57-58, 89-92: x.bfloat16(), then x.norm()): with elem
+// kBF16 the sums take the bf16-rounded values and the norm is rounded to
+// bfloat16 before the safety factor and eps are applied in float32, as the
+// compiled reference evaluates x / (norm * safety + eps).
 //  prepare      the single pass that writes the decayed momentum and the
 //               normalized 16-bit Newton-Schulz input in the orientations the
 //               iteration reads (_matrix_step.py:172-178 and _gram.py:83-87
@@ -41,7 +50,20 @@ struct AccArgs {
   float mu;               // kFullSumsq: momentum decay
   int nesterov;           // kFullSumsq: U = G + mu (M + G) instead of M + G
   int vec;                // float4 path: cols % 4 == 0 and 16-byte aligned rows
+  int round_bf16;         // sums of squares of the bf16-rounded values
 };
+
+__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
+
+__device__ __forceinline__ f32x4 bf16_round4(f32x4 v) {
+  return f32x4{bf16_round(v.x), bf16_round(v.y), bf16_round(v.z), bf16_round(v.w)};
+}
+
+// The normalization denominator of a block from its sum of squares s.
+__device__ __forceinline__ float norm_denom(float s, float safety, float eps, bool round_bf16) {
+  const float norm = round_bf16 ? bf16_round(sqrtf(s)) : sqrtf(s);
+  return norm * safety + eps;
+}
 
 // Four consecutive input elements (float4 index c of a row of IN) as floats,
 // streamed. IN is float, or the 16-bit type of an Orthogonalize input
@@ -94,10 +116,12 @@ __global__ __launch_bounds__(kRowThreads) void accumulate_kernel(AccArgs a) {
       if (MODE == kScores) {
         __builtin_nontemporal_store(s, m4 + c);
         l1 += __builtin_elementwise_abs(s);
-        sq += s * s;
+        const f32x4 r = a.round_bf16 ? bf16_round4(s) : s;
+        sq += r * r;
       } else {
         f32x4 u = s;
         if (a.nesterov) u = gv + s * a.mu;
+        if (a.round_bf16) u = bf16_round4(u);
         sq += u * u;
       }
     };
@@ -125,9 +149,11 @@ __global__ __launch_bounds__(kRowThreads) void accumulate_kernel(AccArgs a) {
       if (MODE == kScores) {
         m[c] = s;
         l1.x += fabsf(s);
-        sq.x += s * s;
+        const float r = a.round_bf16 ? bf16_round(s) : s;
+        sq.x += r * r;
       } else {
         float u = a.nesterov ? gv + s * a.mu : s;
+        if (a.round_bf16) u = bf16_round(u);
         sq.x += u * u;
       }
     }
@@ -144,15 +170,16 @@ __global__ __launch_bounds__(kRowThreads) void accumulate_kernel(AccArgs a) {
   }
 }
 
-// den[b] = sqrt(sum of rowsq over the block's rows) * safety + eps; one wave per block.
+// den[b] = norm_denom(sum of rowsq over the block's rows); one wave per block.
 __global__ __launch_bounds__(64) void block_denom_kernel(const float* rowsq, float* den,
-                                                         int64_t rows, float safety, float eps) {
+                                                         int64_t rows, float safety, float eps,
+                                                         int round_bf16) {
   const int64_t b = blockIdx.x;
   const float* r = rowsq + b * rows;
   float s = 0.f;
   for (int64_t i = threadIdx.x; i < rows; i += kWave) s += r[i];
   s = wave_sum(s);
-  if (threadIdx.x == 0) den[b] = sqrtf(s) * safety + eps;
+  if (threadIdx.x == 0) den[b] = norm_denom(s, safety, eps, round_bf16 != 0);
 }
 
 // ---- prepare: decayed momentum + normalized 16-bit Newton-Schulz input ------
@@ -342,11 +369,13 @@ extern "C" {
 
 int dionw_accumulate_scores(const float* const* grads, int32_t count, int64_t rows_per_tensor,
                             int64_t cols, float* momentum, float* scores, float* row_sumsq,
-                            hipStream_t stream) {
+                            int32_t elem, hipStream_t stream) {
   DIONW_REQUIRE(count >= 0 && rows_per_tensor > 0 && cols > 0,
                 "accumulate_scores: bad sizes (count=%d rows=%lld cols=%lld)", count,
                 (long long)rows_per_tensor, (long long)cols);
   DIONW_REQUIRE(momentum && scores && row_sumsq, "accumulate_scores: null output");
+  DIONW_REQUIRE(elem == kF16 || elem == kBF16 || elem == kF32, "accumulate_scores: bad elem %d",
+                elem);
   for (int32_t start = 0; start < count; start += kMaxTensors) {
     AccArgs a{};
     a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
@@ -361,6 +390,7 @@ int dionw_accumulate_scores(const float* const* grads, int32_t count, int64_t ro
     a.rows_per_tensor = rows_per_tensor;
     a.cols = cols;
     a.vec = table_aligned(a.t, cols) && aligned16(a.momentum);
+    a.round_bf16 = elem == kBF16;
     const int64_t rows = (int64_t)a.t.count * rows_per_tensor;
     DIONW_REQUIRE(rows * kRowThreads <= (int64_t)UINT32_MAX,
                   "accumulate_scores: %lld rows exceed one launch", (long long)rows);
@@ -373,9 +403,10 @@ int dionw_accumulate_scores(const float* const* grads, int32_t count, int64_t ro
 
 int dionw_full_sumsq(const float* const* grads, int32_t count, int64_t rows_per_tensor,
                      int64_t cols, const float* momentum, float mu, int32_t nesterov,
-                     float* row_sumsq, hipStream_t stream) {
+                     float* row_sumsq, int32_t elem, hipStream_t stream) {
   DIONW_REQUIRE(count >= 0 && rows_per_tensor > 0 && cols > 0, "full_sumsq: bad sizes");
   DIONW_REQUIRE(row_sumsq, "full_sumsq: null pointer");
+  DIONW_REQUIRE(elem == kF16 || elem == kBF16 || elem == kF32, "full_sumsq: bad elem %d", elem);
   for (int32_t start = 0; start < count; start += kMaxTensors) {
     AccArgs a{};
     a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
@@ -391,6 +422,7 @@ int dionw_full_sumsq(const float* const* grads, int32_t count, int64_t rows_per_
     a.mu = mu;
     a.nesterov = nesterov;
     a.vec = table_aligned(a.t, cols) && (!a.momentum || aligned16(a.momentum));
+    a.round_bf16 = elem == kBF16;
     const int64_t rows = (int64_t)a.t.count * rows_per_tensor;
     DIONW_REQUIRE(rows * kRowThreads <= (int64_t)UINT32_MAX,
                   "full_sumsq: %lld rows exceed one launch", (long long)rows);
@@ -402,11 +434,12 @@ int dionw_full_sumsq(const float* const* grads, int32_t count, int64_t rows_per_
 }
 
 int dionw_block_denom(const float* row_sumsq, int64_t blocks, int64_t rows, float safety,
-                      float eps, float* den, hipStream_t stream) {
+                      float eps, float* den, int32_t elem, hipStream_t stream) {
   DIONW_REQUIRE(row_sumsq && den && blocks >= 0 && rows > 0, "block_denom: bad arguments");
+  DIONW_REQUIRE(elem == kF16 || elem == kBF16 || elem == kF32, "block_denom: bad elem %d", elem);
   if (blocks == 0) return kOk;
   hipLaunchKernelGGL(block_denom_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, row_sumsq,
-                     den, rows, safety, eps);
+                     den, rows, safety, eps, (int)(elem == kBF16));
   return check_launch("block_denom");
 }
 
@@ -439,6 +472,7 @@ int dionw_normalize_input(const void* x, int32_t x_elem, int64_t blocks, int64_t
   acc.rows_per_tensor = blocks * rows;
   acc.cols = cols;
   acc.vec = vec;
+  acc.round_bf16 = elem == kBF16;
   const dim3 row_grid((unsigned)(blocks * rows));
   if (x_elem == kF32)
     hipLaunchKernelGGL((accumulate_kernel<kFullSumsq, float>), row_grid, dim3(kRowThreads), 0,
@@ -451,7 +485,7 @@ int dionw_normalize_input(const void* x, int32_t x_elem, int64_t blocks, int64_t
                        stream, acc);
   DIONW_TRY(check_launch("normalize_input"));
   hipLaunchKernelGGL(block_denom_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, row_sumsq,
-                     den, rows, safety, eps);
+                     den, rows, safety, eps, (int)(elem == kBF16));
   DIONW_TRY(check_launch("normalize_input"));
   // X = 16-bit(x / den): the every-row prepare pass without momentum writes.
   PrepArgs a{};

@@ -7,7 +7,10 @@
 // the lowest indices. The index set is therefore a pure function of the
 // scores. Outputs come in ascending row order, with the inverse map (slot of
 // each row or -1) that the apply pass reads, and the block's input
-// denominator: sqrt(sum of the selected rows' sums of squares) * safety + eps.
+// denominator: sqrt(sum of the selected rows' sums of squares) * safety + eps,
+// the square root rounded to bfloat16 first when the iteration runs in bfloat16
+// (the reference's quintics take the norm of their bf16 input as a bf16 tensor,
+// _polar_express.py:57-58, 89-92).
 #include "common.h"
 
 namespace dionw {
@@ -24,6 +27,7 @@ struct SelArgs {
   float* den;            // [B]
   int64_t rows, k;
   float safety, eps;
+  int round_bf16;
 };
 
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
@@ -113,7 +117,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   if (tid == 0) {
     float s = 0.f;
     for (int w = 0; w < kSelWaves; ++w) s += wave_part[w];
-    a.den[b] = sqrtf(s) * a.safety + a.eps;
+    const float norm = a.round_bf16 ? (float)(__bf16)sqrtf(s) : sqrtf(s);
+    a.den[b] = norm * a.safety + a.eps;
   }
 }
 
@@ -124,13 +129,14 @@ using namespace dionw;
 
 extern "C" int dionw_select_rows(const float* scores, const float* row_sumsq, int64_t blocks,
                                  int64_t rows, int64_t k, float safety, float eps, int32_t* idx,
-                                 int32_t* slot, float* den, hipStream_t stream) {
+                                 int32_t* slot, float* den, int32_t elem, hipStream_t stream) {
   DIONW_REQUIRE(scores && row_sumsq && idx && slot && den, "select_rows: null pointer");
+  DIONW_REQUIRE(elem == kF16 || elem == kBF16 || elem == kF32, "select_rows: bad elem %d", elem);
   DIONW_REQUIRE(rows > 0 && k > 0 && k <= rows && rows < (int64_t)1 << 31,
                 "select_rows: need 0 < k <= rows < 2^31 (k=%lld rows=%lld)", (long long)k,
                 (long long)rows);
   if (blocks == 0) return kOk;
-  SelArgs a{scores, row_sumsq, idx, slot, den, rows, k, safety, eps};
+  SelArgs a{scores, row_sumsq, idx, slot, den, rows, k, safety, eps, (int)(elem == kBF16)};
   hipLaunchKernelGGL(select_kernel, dim3((unsigned)blocks), dim3(kSelThreads), 0, stream, a);
   return check_launch("select_rows");
 }

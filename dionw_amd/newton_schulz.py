@@ -12,8 +12,13 @@ steps each, on the MFMA kernels of ``libdionw_hip.so``:
   quintic, input scaled by 1.02 times its norm;
 - ``KELLER`` / ``KELLER_TRITON``: Keller Jordan's bfloat16 quintic.
 
-The cuBLAS and Triton variants of the reference differ only in how their
-products round; here both run the same symmetric-product kernels.
+The two variants of each quintic differ in where they round, and keep the
+reference's difference (_polar_express.py:43-104): the ``_TRITON`` kinds round
+each line once (``c A A + b A`` and ``a X + P X`` from float32 accumulators),
+the others round the products ``A A`` and ``P X`` to bfloat16 before the
+elementwise terms, as separate cuBLAS products do. Both run the same symmetric
+MFMA products; a tall block is iterated in its wide orientation, whose products
+are the transposes of the reference's right-hand ones.
 """
 
 from __future__ import annotations
@@ -35,7 +40,7 @@ __all__ = ["NewtonSchulz", "Orthogonalize", "HipOrthogonalize", "newton_schulz_f
 Orthogonalize = Callable[[Tensor, float], Tensor]
 
 # Library kinds (include/dionw_hip.h, dionw_newton_schulz).
-_GRAM, _POLAR_EXPRESS, _KELLER = 0, 1, 2
+_GRAM, _PE_TRITON, _KELLER_TRITON, _PE_CUBLAS, _KELLER_CUBLAS = 0, 1, 2, 3, 4
 # Input types dionw_normalize_input reads as they are.
 _INPUT_ELEMS = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -261,14 +266,14 @@ def run_newton_schulz_group(calls: list[NewtonSchulzCall], stream: int) -> None:
 _KINDS: dict[NewtonSchulz, HipOrthogonalize] = {
     NewtonSchulz.GRAM: HipOrthogonalize(NewtonSchulz.GRAM, _GRAM, torch.float16, 1.0),
     NewtonSchulz.POLAR_EXPRESS: HipOrthogonalize(
-        NewtonSchulz.POLAR_EXPRESS, _POLAR_EXPRESS, torch.bfloat16, 1.02
+        NewtonSchulz.POLAR_EXPRESS, _PE_CUBLAS, torch.bfloat16, 1.02
     ),
     NewtonSchulz.POLAR_EXPRESS_TRITON: HipOrthogonalize(
-        NewtonSchulz.POLAR_EXPRESS_TRITON, _POLAR_EXPRESS, torch.bfloat16, 1.02
+        NewtonSchulz.POLAR_EXPRESS_TRITON, _PE_TRITON, torch.bfloat16, 1.02
     ),
-    NewtonSchulz.KELLER: HipOrthogonalize(NewtonSchulz.KELLER, _KELLER, torch.bfloat16, 1.0),
+    NewtonSchulz.KELLER: HipOrthogonalize(NewtonSchulz.KELLER, _KELLER_CUBLAS, torch.bfloat16, 1.0),
     NewtonSchulz.KELLER_TRITON: HipOrthogonalize(
-        NewtonSchulz.KELLER_TRITON, _KELLER, torch.bfloat16, 1.0
+        NewtonSchulz.KELLER_TRITON, _KELLER_TRITON, torch.bfloat16, 1.0
     ),
 }
 

@@ -32,8 +32,18 @@ typedef struct ihipStream_t* dionw_stream_t; /* hipStream_t */
 /* Last error message of the calling thread ("" when none). */
 const char* dionw_last_error(void);
 
-/* ABI revision of this header (1). */
+/* ABI revision of this header (2). */
 int dionw_abi_version(void);
+
+/*
+ * Norm element type (the `elem` argument of the functions that form the
+ * Newton-Schulz normalization): the element code of the iteration the sums
+ * normalize. 0 (float16 Gram) and 2: sums of squares of the float32 values and
+ * den = sqrt(sum) * safety + eps (the norm of x.float(), _gram.py:85-86).
+ * 1 (bfloat16 quintics): sums of squares of the values rounded to bfloat16 and
+ * den = float(bf16(sqrt(sum))) * safety + eps, the norm of the bf16 input taken
+ * as a bf16 tensor (_polar_express.py:57-58, 89-92).
+ */
 
 /*
  * M += G for every row of a run, with each row's l1 norm (the top-k score) and
@@ -43,10 +53,11 @@ int dionw_abi_version(void);
  * column order, then an xor butterfly over the 64 lanes).
  *   grads[count]: float32 gradients, rows_per_tensor x cols each, contiguous.
  *   momentum: [count * rows_per_tensor, cols]; scores, row_sumsq: one per row.
+ *   elem: the norm element type (row_sumsq of the bf16-rounded sums when 1).
  */
 int dionw_accumulate_scores(const float* const* grads, int32_t count, int64_t rows_per_tensor,
                             int64_t cols, float* momentum, float* scores, float* row_sumsq,
-                            dionw_stream_t stream);
+                            int32_t elem, dionw_stream_t stream);
 
 /*
  * Per-row sum of squares of the every-row Newton-Schulz input U = M + G
@@ -57,19 +68,21 @@ int dionw_accumulate_scores(const float* const* grads, int32_t count, int64_t ro
  */
 int dionw_full_sumsq(const float* const* grads, int32_t count, int64_t rows_per_tensor,
                      int64_t cols, const float* momentum, float mu, int32_t nesterov,
-                     float* row_sumsq, dionw_stream_t stream);
+                     float* row_sumsq, int32_t elem, dionw_stream_t stream);
 
-/* den[b] = sqrt(sum of row_sumsq over block b's rows) * safety + eps: the
- * Frobenius normalization of _gram.py:86 (safety 1) and _polar_express.py:92
- * (safety 1.02 for Polar Express, 1 for Keller). */
+/* den[b] = sqrt(sum of row_sumsq over block b's rows) * safety + eps (the
+ * square root rounded to bf16 first for elem 1): the Frobenius normalization
+ * of _gram.py:86 (safety 1) and _polar_express.py:92 (safety 1.02 for Polar
+ * Express, 1 for Keller). */
 int dionw_block_denom(const float* row_sumsq, int64_t blocks, int64_t rows, float safety,
-                      float eps, float* den, dionw_stream_t stream);
+                      float eps, float* den, int32_t elem, dionw_stream_t stream);
 
 /*
  * The normalization prologue of the Orthogonalize plugin on a contiguous
  * [blocks, rows, cols] input x of elem x_elem (0 fp16, 1 bf16, 2 fp32), read
  * as it is: row sums of squares as dionw_full_sumsq forms them (into
- * row_sumsq, blocks * rows floats), den as dionw_block_denom, then
+ * row_sumsq, blocks * rows floats), den as dionw_block_denom (both with the
+ * norm element type elem), then
  * X = 16-bit(x / den) of type elem (0 or 1) written as dionw_prepare_ns_input
  * writes it in every-row mode without momentum (out_rowmajor and/or
  * out_transposed, padded to p_pad x j_pad). Bit-identical to those three calls
@@ -87,11 +100,11 @@ int dionw_normalize_input(const void* x, int32_t x_elem, int64_t blocks, int64_t
  * Exact: ties at the k-th score take the lowest row indices.
  *   idx [blocks, k]: selected rows, ascending; slot [blocks, rows]: position
  *   of each row in idx or -1; den [blocks]: sqrt(sum of the selected rows'
- *   row_sumsq) * safety + eps.
+ *   row_sumsq) * safety + eps, as dionw_block_denom forms it for elem.
  */
 int dionw_select_rows(const float* scores, const float* row_sumsq, int64_t blocks, int64_t rows,
                       int64_t k, float safety, float eps, int32_t* idx, int32_t* slot,
-                      float* den, dionw_stream_t stream);
+                      float* den, int32_t elem, dionw_stream_t stream);
 
 /*
  * One pass writing the decayed momentum and the Newton-Schulz input.
@@ -120,8 +133,11 @@ int dionw_prepare_ns_input(const float* const* grads, int32_t count, float* mome
  * rounding). A [m, k], B [n, k], D and C [m, n], all row-major with the given
  * leading dimensions and batch strides (elements); ct (optional) receives C^T
  * [n, m]. symmetric: only the tiles on and above the diagonal are computed and
- * mirrored (m == n, output c only). elem 0 or 1; k, lda, ldb and the operand
- * batch strides must be multiples of 8.
+ * mirrored (m == n, output c only). elem 0 or 1: k, lda, ldb and the operand
+ * batch strides must be multiples of 8 and the operands 16-byte aligned.
+ * elem 2: float32 operands and output, products and sums in float32 on the
+ * fp32 MFMA (the reference's "ieee" dot for float32 inputs), any sizes and
+ * strides.
  * Replaces ns_line_1 (alpha A A^T, _symmetric_kernels.py:252-277), ns_line_2
  * (c A A^T + b A, :280-312) and the baddbmm/bmm products of _gram.py:46-69
  * and _polar_express.py:98-103.
@@ -132,6 +148,15 @@ int dionw_gemm_nt(int32_t elem, int64_t batch, int64_t m, int64_t n, int64_t k, 
                   int64_t ldc, int64_t stride_c, void* ct, int64_t ldct, int64_t stride_ct,
                   int32_t symmetric, dionw_stream_t stream);
 
+/*
+ * The five (a, b, c) rows dionw_newton_schulz uses for kind (out: 15 doubles,
+ * row-major; the kernels take them rounded to float): the Gram table of
+ * _gram.py:24-35 with the 1.05 safety folded in as (a/s, b/s^3, c/s^5), the
+ * Polar Express table of _polar_express.py:28-34, Keller's row of
+ * _keller.py:20. Host only: no device work.
+ */
+int dionw_ns_coefficients(int32_t kind, double* out);
+
 /* Workspace bytes dionw_newton_schulz needs. */
 size_t dionw_newton_schulz_workspace(int32_t kind, int64_t batch, int64_t r, int64_t c);
 
@@ -141,8 +166,11 @@ size_t dionw_newton_schulz_workspace(int32_t kind, int64_t batch, int64_t r, int
  *   kind 0 (GRAM): fp16 Gram Newton-Schulz with restart at iteration 2 when
  *     c > r (_gram.py:50-69), the standard Polar Express iteration when
  *     c == r (_gram.py:41-47); output bf16(fp16(.)).
- *   kind 1 (POLAR_EXPRESS) / 2 (KELLER): the bf16 quintic (_polar_express.py:
- *     74-104; _keller.py:20-34).
+ *   kind 1 (POLAR_EXPRESS_TRITON) / 2 (KELLER_TRITON): the bf16 quintic with
+ *     each line rounded once (_polar_express.py:74-104; _keller.py:20-34).
+ *   kind 3 (POLAR_EXPRESS) / 4 (KELLER): the bf16 quintic with the products
+ *     A A and P X rounded to bf16 before the elementwise terms, as the
+ *     reference's cuBLAS variant computes it (_polar_express.py:43-71).
  *   x [batch, r, c] and xt [batch, c, r] (the input and its transpose, both
  *   overwritten), r <= c multiples of 8. With r a multiple of 32 the products
  *   read x itself where they multiply it from the left: xt is then neither

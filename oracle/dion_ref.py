@@ -167,37 +167,77 @@ def gram_polar_express(matrix: Tensor, epsilon: float) -> Tensor:
     return (x.mT if tall else x).bfloat16()
 
 
+def _bf16_normalized(x: Tensor, epsilon: float, norm_safety: float) -> Tensor:
+    """``x / (x.norm() * safety + eps)`` of bfloat16 ``x`` as the compiled
+    reference evaluates it (_polar_express.py:57-58, 89-92): the norm is a
+    float32 sum of the bf16 values stored as a bf16 tensor; the scaling and the
+    division run in float32 and round once to bfloat16."""
+    xf = x.float()
+    norm = torch.linalg.vector_norm(xf, dim=(-2, -1), keepdim=True).bfloat16().float()
+    return (xf / (norm * norm_safety + epsilon)).bfloat16()
+
+
 def quintic(
     matrix: Tensor, epsilon: float, coefficients: tuple, norm_safety: float
 ) -> Tensor:
-    """quintic_triton (_polar_express.py:74-104) in bfloat16."""
+    """quintic_triton (_polar_express.py:74-104) in bfloat16: each line's product
+    and elementwise terms from one float32 accumulation, rounded once."""
     tall = matrix.size(-2) > matrix.size(-1)
     x = matrix.to(torch.bfloat16)
     if tall:
         x = x.mT
-    xf = x.float()
-    norm = torch.linalg.vector_norm(xf, dim=(-2, -1), keepdim=True)
-    x = (xf / (norm * norm_safety + epsilon)).bfloat16().contiguous()
+    x = _bf16_normalized(x, epsilon, norm_safety).contiguous()
     for a, b, c in coefficients:
         poly = ns_line_2(ns_line_1(x), c, b)
         x = _baddbmm(x, poly, x, a)
     return x.mT if tall else x
 
 
+def quintic_cublas(
+    matrix: Tensor, epsilon: float, coefficients: tuple, norm_safety: float
+) -> Tensor:
+    """quintic_cublas (_polar_express.py:43-71) in bfloat16: every product is
+    rounded to bfloat16 on its own (cuBLAS), and the elementwise terms
+    ``b A + c (A A)`` and ``a x + (...)`` combine those bf16 products in float32
+    with one rounding each (inductor fuses them). A tall block multiplies from
+    the right (``x^T x``, ``x P``), a wide or square one from the left."""
+    x = _bf16_normalized(matrix.to(torch.bfloat16), epsilon, norm_safety)
+    tall = matrix.size(-2) > matrix.size(-1)
+    for a, b, c in coefficients:
+        gram = (_mm(x.mT, x) if tall else _mm(x, x.mT)).bfloat16()
+        gram2 = _mm(gram, gram).bfloat16()
+        poly = (b * gram.float() + c * gram2.float()).bfloat16()
+        product = (_mm(x, poly) if tall else _mm(poly, x)).bfloat16()
+        x = (a * x.float() + product.float()).bfloat16()
+    return x
+
+
 def polar_express(matrix: Tensor, epsilon: float) -> Tensor:
+    """POLAR_EXPRESS (_polar_express.py:107-112): the cuBLAS quintic."""
+    return quintic_cublas(matrix, epsilon, POLAR_EXPRESS_COEFFICIENTS, POLAR_EXPRESS_NORM_SAFETY)
+
+
+def polar_express_triton(matrix: Tensor, epsilon: float) -> Tensor:
+    """POLAR_EXPRESS_TRITON (_polar_express.py:115-120)."""
     return quintic(matrix, epsilon, POLAR_EXPRESS_COEFFICIENTS, POLAR_EXPRESS_NORM_SAFETY)
 
 
 def keller(matrix: Tensor, epsilon: float) -> Tensor:
+    """KELLER (_keller.py:25-28): the cuBLAS quintic."""
+    return quintic_cublas(matrix, epsilon, KELLER_COEFFICIENTS, KELLER_NORM_SAFETY)
+
+
+def keller_triton(matrix: Tensor, epsilon: float) -> Tensor:
+    """KELLER_TRITON (_keller.py:31-34)."""
     return quintic(matrix, epsilon, KELLER_COEFFICIENTS, KELLER_NORM_SAFETY)
 
 
 ORTHOGONALIZE = {
     "gram": gram_polar_express,
     "polar_express": polar_express,
-    "polar_express_triton": polar_express,
+    "polar_express_triton": polar_express_triton,
     "keller": keller,
-    "keller_triton": keller,
+    "keller_triton": keller_triton,
 }
 
 

@@ -12,7 +12,9 @@ package), so the vectors come from the oracle's restatement of its PyTorch path
   ~N(0, 0.02^2), gradient ~N(0, 1e-3^2), zero momentum, seed 0, fraction 1
   (NorMuon, the standard iteration of Gram Newton-Schulz on a square block),
   momentum 0.95, muon_beta2 0.95, lr 3e-4, weight decay 0.05: the variance, a
-  64x64 corner of the updated weight, and norms of the update.
+  64x64 corner of the updated weight, norms, and the whole update
+  ``W_new - W (1 - lr wd)`` as float16 of update / max|update| (quantization
+  ~3e-4 relative Frobenius, far below the 1e-2 bar it is held to).
 
 Usage: python tests/golden/make_fixtures.py
 """
@@ -75,7 +77,10 @@ def config1_expected():
     dion_ref.step_blocks(wb, grad[None], m, v, k=1024, lr=3e-4, mu=0.95, beta2=0.95,
                          weight_decay=0.05, kind="gram")
     update = wb[0] - start * (1.0 - 3e-4 * 0.05)
+    scale = float(update.abs().max())
     return {
+        "update_f16": (update / scale).numpy().astype(np.float16),
+        "update_scale": np.float64(scale),
         "variance": v[0, :, 0].numpy().copy(),
         "weight_corner": wb[0, :64, :64].numpy().copy(),
         "update_norm": np.float64(update.double().norm()),
@@ -86,7 +91,7 @@ def config1_expected():
 
 def main() -> None:
     np.savez(HERE / "small_step.npz", **small_expected())
-    np.savez(HERE / "config1.npz", **config1_expected())
+    np.savez_compressed(HERE / "config1.npz", **config1_expected())
     print("wrote", HERE / "small_step.npz", HERE / "config1.npz")
 
 

@@ -2,8 +2,8 @@
 
 CPU: the oracle still reproduces them (bit-exact for scores, indices and
 momentum). GPU: the HIP step reproduces them — exact polar factor: weights to
-float32 rounding; the 1024x1024 NorMuon step of config1.npz: update within 1e-2
-relative, variance within 2e-2, momentum exact.
+float32 rounding; the 1024x1024 NorMuon step of config1.npz: the whole update
+within 1e-2 relative Frobenius, variance within 2e-2, momentum exact.
 """
 
 from __future__ import annotations
@@ -41,6 +41,12 @@ def test_oracle_reproduces_config1_fixture() -> None:
     assert got["momentum_abs_sum"] == want["momentum_abs_sum"]
     np.testing.assert_allclose(got["weight_corner"], want["weight_corner"], rtol=0, atol=1e-7)
     np.testing.assert_allclose(got["update_norm"], want["update_norm"], rtol=1e-6)
+    assert np.array_equal(got["update_f16"], want["update_f16"])
+    assert got["update_scale"] == want["update_scale"]
+
+
+def _fixture_update(want: dict) -> np.ndarray:
+    return want["update_f16"].astype(np.float64) * float(want["update_scale"])
 
 
 @pytest.mark.gpu
@@ -91,6 +97,9 @@ def test_hip_step_matches_config1_fixture() -> None:
     corner_got = update[:64, :64].numpy()
     rel = np.linalg.norm(corner_got - corner_ref) / np.linalg.norm(corner_ref)
     assert rel < 2e-2, rel
+    whole_ref = _fixture_update(want)
+    rel_whole = np.linalg.norm(update.double().numpy() - whole_ref) / np.linalg.norm(whole_ref)
+    assert rel_whole < 1e-2, rel_whole
     var = opt.state[p]["variance"].cpu().numpy()[:, 0]
     rel_v = np.linalg.norm(var - want["variance"]) / np.linalg.norm(want["variance"])
     assert rel_v < 2e-2, rel_v

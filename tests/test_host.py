@@ -8,6 +8,8 @@ structural checks of load_state_dict (tests/test_optimizer.py:776-798).
 from __future__ import annotations
 
 import ctypes
+import json
+import math
 import re
 from pathlib import Path
 
@@ -30,7 +32,78 @@ def test_library_exports_every_declared_symbol() -> None:
     lib = ctypes.CDLL(str(_lib.library_path()))
     for name in declared:
         assert hasattr(lib, name), f"{name} not exported"
-    assert _lib.library().dionw_abi_version() == 1
+    assert _lib.library().dionw_abi_version() == 2
+
+
+@pytest.mark.parametrize(("kind", "table"), [(0, "gram"), (1, "polar_express"), (2, "keller"),
+                                             (3, "polar_express"), (4, "keller")])
+def test_library_coefficient_tables_equal_the_reference_literals(kind: int, table: str) -> None:
+    """The five (a, b, c) rows each library kind runs against the reference's
+    literal tables (tests/golden/coefficients.json); the Gram rows with the
+    safety factor folded in as _gram.py:32-35 does."""
+    fx = json.loads((Path(__file__).resolve().parent / "golden" / "coefficients.json").read_text())
+    if table == "gram":
+        s = fx["gram_safety"]
+        want = [(a / s, b / s**3, c / s**5) for a, b, c in fx["gram_unmodified"]]
+    else:
+        want = [tuple(r) for r in fx[table]]
+    out = (ctypes.c_double * 15)()
+    _lib.call("dionw_ns_coefficients", kind, out)
+    got = [tuple(out[3 * i:3 * i + 3]) for i in range(5)]
+    for row_got, row_want in zip(got, want, strict=True):
+        for g, w in zip(row_got, row_want):
+            assert math.isclose(g, w, rel_tol=1e-15), (kind, got, want)
+    with pytest.raises(ValueError, match="unknown kind"):
+        _lib.call("dionw_ns_coefficients", 5, out)
+
+
+def test_gemm_nt_rejects_mismatched_operands() -> None:
+    """gemm_nt checks shapes, batches, dtypes and devices on the host before any
+    launch (a mismatched operand would otherwise be read or written out of
+    bounds)."""
+    from dionw_amd._kernels import gemm_nt
+
+    a = torch.zeros(2, 64, 32, dtype=torch.float16)
+    with pytest.raises(ValueError, match="does not match"):
+        gemm_nt(a, torch.zeros(2, 64, 48, dtype=torch.float16))      # k differs
+    with pytest.raises(ValueError, match="does not match"):
+        gemm_nt(a, torch.zeros(3, 64, 32, dtype=torch.float16))      # batch differs
+    with pytest.raises(ValueError, match="both be 2-D or 3-D"):
+        gemm_nt(a, torch.zeros(64, 32, dtype=torch.float16))
+    b = torch.zeros(2, 40, 32, dtype=torch.float16)
+    with pytest.raises(ValueError, match="out must be"):
+        gemm_nt(a, b, out=torch.zeros(2, 64, 41, dtype=torch.float16))
+    with pytest.raises(ValueError, match="out_t must be"):
+        gemm_nt(a, b, out_t=torch.zeros(2, 64, 40, dtype=torch.float16))
+    with pytest.raises(ValueError, match="d must be"):
+        gemm_nt(a, b, d=torch.zeros(2, 40, 64, dtype=torch.float16), beta=1.0)
+    with pytest.raises(ValueError, match="share a's dtype"):
+        gemm_nt(a, b.to(torch.bfloat16))
+    with pytest.raises(ValueError, match="unit column stride"):
+        gemm_nt(a, torch.zeros(2, 32, 40, dtype=torch.float16).mT)
+    with pytest.raises(ValueError, match="unsupported dtype"):
+        gemm_nt(a.double(), b.double())
+    with pytest.raises(ValueError, match="symmetric"):
+        gemm_nt(a, b, symmetric=True)
+
+
+def test_momentum_seams_take_any_float_gradient_and_reject_others() -> None:
+    """accumulate_row_l1 / accumulate_copy_decay accept float16, bfloat16 and
+    float32 gradients like the reference's kernels (_momentum_kernels.py:89-133);
+    integer gradients and mismatched sizes are rejected before any launch."""
+    from dionw_amd._kernels import _check
+
+    m = torch.zeros(4, 8)
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        g = torch.randn(4, 8).to(dtype)
+        got = _check(g, m)
+        assert got.dtype == torch.float32 and torch.equal(got, g.float())
+    with pytest.raises(ValueError, match="float gradient"):
+        _check(torch.zeros(4, 8, dtype=torch.int32), m)
+    with pytest.raises(ValueError, match="float32 momentum"):
+        _check(torch.zeros(4, 9), m)
+    with pytest.raises(ValueError, match="contiguous"):
+        _check(torch.zeros(8, 4).mT, m)
 
 
 def test_grouped_newton_schulz_rejects_overlapping_workspaces() -> None:

@@ -45,13 +45,15 @@ def test_accumulate_scores_bit_exact(rows: int, cols: int) -> None:
     np.testing.assert_allclose(got, brute, rtol=1e-5)
 
 
-def _select(scores: torch.Tensor, rowsq: torch.Tensor, k: int):
+def _select(scores: torch.Tensor, rowsq: torch.Tensor, k: int, *, elem: int = _lib.F16,
+            safety: float = 1.0):
     blocks, rows = scores.shape
     idx = torch.empty(blocks, k, dtype=torch.int32, device=DEV)
     slot = torch.empty(blocks, rows, dtype=torch.int32, device=DEV)
     den = torch.empty(blocks, device=DEV)
-    _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k, 1.0,
-              1e-8, idx.data_ptr(), slot.data_ptr(), den.data_ptr(), _lib.stream_handle())
+    _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k, safety,
+              1e-8, idx.data_ptr(), slot.data_ptr(), den.data_ptr(), elem,
+              _lib.stream_handle())
     torch.cuda.synchronize()
     return idx.cpu().numpy(), slot.cpu().numpy(), den.cpu()
 
@@ -194,9 +196,9 @@ def test_normalize_input_reads_16bit_inputs(x_dtype, elem: int, blocks: int, row
         else:
             grads = _lib.ptr_array([src])
             _lib.call("dionw_full_sumsq", grads, 1, blocks * rows, cols, None, 0.0, 0,
-                      rowsq.data_ptr(), st)
+                      rowsq.data_ptr(), elem, st)
             _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, 1.02, 1e-7,
-                      den.data_ptr(), st)
+                      den.data_ptr(), elem, st)
             _lib.call("dionw_prepare_ns_input", grads, 1, None, None, den.data_ptr(), blocks,
                       rows, cols, rows, p_pad, j_pad, 0.0, 0, 0, elem, xr.data_ptr(),
                       xt.data_ptr(), st)
@@ -249,6 +251,46 @@ def test_gemm_nt_matches_fp32(dtype: torch.dtype, batch: int, m: int, n: int, k:
 @pytest.mark.parametrize("shape", [(3, 64, 256), (3, 128, 128), (96, 160), (2, 520, 1032)])
 def test_symmetric_products(dtype: torch.dtype, shape: tuple[int, ...]) -> None:
     _check_symmetric(dtype, shape)
+
+
+@pytest.mark.parametrize("shape", [(3, 64, 256), (2, 100, 70), (130, 37), (2, 520, 1032)])
+def test_float32_symmetric_products(shape: tuple[int, ...]) -> None:
+    """float32 ns_line_1 / ns_line_2 (the reference's "ieee" path for float32
+    inputs, _symmetric_kernels.py:275, 311) on the fp32 MFMA: within float32
+    rounding of float64 products, exactly symmetric, any size."""
+    g = _gen(14)
+    x = torch.randn(*shape, generator=g) / shape[-1] ** 0.5
+    gram = _kernels.ns_line_1(x.to(DEV))
+    torch.cuda.synchronize()
+    assert gram.dtype == torch.float32
+    ref = x.double() @ x.double().mT
+    assert rel_fro(gram.cpu(), ref) < 1e-6, f"ns_line_1 fp32 {shape}"
+    assert torch.equal(gram.cpu(), gram.cpu().mT), "ns_line_1 fp32 output not exactly symmetric"
+    poly = _kernels.ns_line_2(gram, alpha=0.5, beta=-1.5)
+    torch.cuda.synchronize()
+    g64 = gram.cpu().double()
+    ref2 = 0.5 * (g64 @ g64) - 1.5 * g64
+    assert rel_fro(poly.cpu(), ref2) < 1e-6, f"ns_line_2 fp32 {shape}"
+    assert torch.equal(poly.cpu(), poly.cpu().mT)
+
+
+def test_float32_gemm_with_transposed_output_and_strides() -> None:
+    """A float32 product of operands with padded row strides, an addend and a
+    transposed second output, against float64."""
+    g = _gen(15)
+    a = torch.randn(2, 70, 50, generator=g)
+    b = torch.randn(2, 90, 50, generator=g)
+    d = torch.randn(2, 70, 90, generator=g)
+    a_pad = torch.zeros(2, 70, 56)
+    a_pad[..., :50] = a
+    a_d = a_pad.to(DEV)[..., :50]
+    out_t = torch.empty(2, 90, 70, device=DEV)
+    out = _kernels.gemm_nt(a_d, b.to(DEV), d=d.to(DEV), alpha=0.7, beta=-1.3, out_t=out_t,
+                           out=torch.empty(2, 70, 90, device=DEV))
+    torch.cuda.synchronize()
+    ref = 0.7 * (a.double() @ b.double().mT) - 1.3 * d.double()
+    assert rel_fro(out.cpu(), ref) < 1e-6
+    assert torch.equal(out_t.cpu(), out.cpu().mT)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -323,6 +365,57 @@ def test_newton_schulz_matches_oracle(kind: NewtonSchulz, shape: tuple[int, ...]
     polar_bar = 0.3 if kind in (NewtonSchulz.KELLER, NewtonSchulz.KELLER_TRITON) else 0.2
     exact_err = rel_fro(out.cpu().float(), dion_ref.exact_polar(x))
     assert exact_err < polar_bar, f"{kind.value} {shape}: {exact_err} from the exact polar factor"
+
+
+@pytest.mark.parametrize(("cublas", "triton"), [
+    (NewtonSchulz.POLAR_EXPRESS, NewtonSchulz.POLAR_EXPRESS_TRITON),
+    (NewtonSchulz.KELLER, NewtonSchulz.KELLER_TRITON)])
+@pytest.mark.parametrize("shape", [(2, 256, 1024), (2, 1024, 256)])
+def test_quintic_variants_round_as_their_reference_twins(cublas, triton, shape) -> None:
+    """The two quintic variants round at different points (_polar_express.py:
+    43-104): each HIP kind is much closer to its own oracle than to the other
+    variant's, so the products really are rounded where the variant says."""
+    g = _gen(16)
+    x = torch.randn(*shape, generator=g)
+    for kind, other in ((cublas, triton), (triton, cublas)):
+        out = newton_schulz_fn(kind)(x.to(DEV), 1e-8)
+        torch.cuda.synchronize()
+        same = rel_fro(out.cpu().float(), dion_ref.ORTHOGONALIZE[kind.value](x, 1e-8).float())
+        cross = rel_fro(out.cpu().float(), dion_ref.ORTHOGONALIZE[other.value](x, 1e-8).float())
+        assert same < 0.5 * cross, f"{kind.value} {shape}: own oracle {same}, other {cross}"
+
+
+def test_bf16_norms_round_as_the_quintics() -> None:
+    """With the bf16 norm element type the row sums of squares are of the
+    bf16-rounded momentum and the denominator is bf16(sqrt(sum)) * safety + eps
+    (_polar_express.py:57-58); the l1 scores are unchanged."""
+    g = _gen(17)
+    blocks, rows, cols, k = 2, 300, 512, 75
+    grad = torch.randn(blocks * rows, cols, generator=g)
+    mom = torch.randn(blocks * rows, cols, generator=g)
+    st = _lib.stream_handle()
+    out = {}
+    for elem in (_lib.F16, _lib.BF16):
+        m_d = mom.to(DEV)
+        scores = torch.empty(blocks * rows, device=DEV)
+        rowsq = torch.empty(blocks * rows, device=DEV)
+        _lib.call("dionw_accumulate_scores", _lib.ptr_array([grad.to(DEV)]), 1, blocks * rows,
+                  cols, m_d.data_ptr(), scores.data_ptr(), rowsq.data_ptr(), elem, st)
+        idx, _, den = _select(scores.view(blocks, rows), rowsq.view(blocks, rows), k, elem=elem,
+                              safety=1.02)
+        out[elem] = (scores.cpu(), rowsq.cpu(), idx, den)
+    assert torch.equal(out[_lib.F16][0], out[_lib.BF16][0]), "scores depend on the norm type"
+    summed = (mom + grad)
+    want_sq = summed.bfloat16().double().square().sum(-1)
+    assert rel_fro(out[_lib.BF16][1], want_sq) < 1e-6
+    want_sq32 = summed.double().square().sum(-1)
+    assert rel_fro(out[_lib.F16][1], want_sq32) < 1e-6
+    for b in range(blocks):
+        rows_b = torch.from_numpy(out[_lib.BF16][2][b]).long()
+        s = float(out[_lib.BF16][1].view(blocks, rows)[b, rows_b].double().sum())
+        norm = float(torch.tensor(s ** 0.5, dtype=torch.float32).bfloat16().float())
+        want_den = norm * 1.02 + 1e-8
+        assert abs(float(out[_lib.BF16][3][b]) - want_den) <= 2e-6 * want_den, b
 
 
 @pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 1024, 4096)])

@@ -110,7 +110,14 @@ def _exact_polar_cpu(x: torch.Tensor, epsilon: float) -> torch.Tensor:
     ((100, 70), 0.3, None, 3e-2)])
 def test_hip_step_matches_oracle(kind, shape, fraction, heads, bar) -> None:
     """The full HIP step (Newton-Schulz included) against the oracle: selection
-    and momentum bit-exact, the update within the Newton-Schulz rounding."""
+    and momentum bit-exact, the update within the Newton-Schulz rounding.
+
+    POLAR_EXPRESS rounds its products to bf16 before the elementwise terms (the
+    reference's cuBLAS quintic), which puts it ~0.03 from the float64 polynomial
+    where the other kinds are at 0.003-0.015 (tests/test_oracle.py), so its
+    update bar is twice the others'."""
+    if kind is NewtonSchulz.POLAR_EXPRESS:
+        bar = 2 * bar
     g = torch.Generator().manual_seed(1)
     start = torch.randn(*shape, generator=g) * 0.02
     param = nn.Parameter(start.clone().to(DEV))

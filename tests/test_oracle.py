@@ -7,7 +7,9 @@ fails it.
 
 from __future__ import annotations
 
+import json
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -15,6 +17,9 @@ import torch
 
 from oracle import dion_ref
 from tests.conftest import rel_fro
+
+COEFFICIENTS = json.loads(
+    (Path(__file__).resolve().parent / "golden" / "coefficients.json").read_text())
 
 
 @pytest.mark.parametrize(("rows", "cols"), [(37, 3000), (8, 4096), (5, 1001), (3, 6), (2, 64)])
@@ -49,11 +54,64 @@ def test_topk_rows_sets_and_ties() -> None:
     assert np.array_equal(dion_ref.topk_rows(tied, 4), [0, 1, 2, 7])
 
 
-def test_gram_coefficients_fold_the_safety_factor() -> None:
-    a, b, c = dion_ref.GRAM_COEFFICIENTS[0]
-    assert math.isclose(a * 1.05, 8.28721201814563)
-    assert math.isclose(b * 1.05**3, -23.595886519098837)
-    assert math.isclose(c * 1.05**5, 17.300387312530933)
+def test_coefficient_tables_equal_the_reference_literals() -> None:
+    """Every row of the Gram, Polar Express and Keller tables against the
+    literals of the reference's source (tests/golden/coefficients.json, parsed
+    from _gram.py:24-37, _polar_express.py:28-36, _keller.py:20-22)."""
+    fx = COEFFICIENTS
+    s = fx["gram_safety"]
+    folded = tuple((a / s, b / s**3, c / s**5) for a, b, c in fx["gram_unmodified"])
+    assert len(folded) == 5
+    assert dion_ref.GRAM_COEFFICIENTS == folded
+    assert dion_ref.GRAM_RESTART_ITERATION == fx["gram_restart_iteration"]
+    assert [list(r) for r in dion_ref.POLAR_EXPRESS_COEFFICIENTS] == fx["polar_express"]
+    assert dion_ref.POLAR_EXPRESS_NORM_SAFETY == fx["polar_express_norm_safety"]
+    assert [list(r) for r in dion_ref.KELLER_COEFFICIENTS] == fx["keller"]
+    assert dion_ref.KELLER_NORM_SAFETY == fx["keller_norm_safety"]
+
+
+@pytest.mark.parametrize("n", [256, 1024])
+def test_standard_iteration_vs_float64_polynomial(n: int) -> None:
+    """The standard iteration on square blocks (_gram.py:41-47) against the same
+    five polynomials in float64. The bar is the rounding it performs: the bf16
+    output alone is ~2.3e-3 relative (unit roundoff 2^-8 / sqrt 3), plus 15
+    float16 roundings of the iterate's lines (2^-11 / sqrt 3 each) compounding
+    through the iteration; a dropped term or a wrong coefficient is off by far
+    more (>5e-2)."""
+    x = torch.randn(1, n, n, generator=torch.Generator().manual_seed(10 + n))
+    target = dion_ref.polynomial_float64(x, dion_ref.GRAM_COEFFICIENTS, 1.0)
+    err = rel_fro(dion_ref.gram_polar_express(x, 1e-7).float(), target)
+    bar = 2 ** -8 / math.sqrt(3) + 15 * 2 ** -11 / math.sqrt(3)
+    assert err < bar, (err, bar)
+
+
+@pytest.mark.parametrize("shape", [(2, 96, 256), (2, 256, 96), (1, 128, 128)])
+def test_cublas_quintic_vs_float64_polynomial(shape) -> None:
+    """quintic_cublas (_polar_express.py:43-71) for both tables against the
+    float64 polynomial, and a tall block (iterated from the right) against the
+    transposed wide block: the same products, so equal to the rounding.
+
+    Rounding A A to bf16 before scaling it by c (15.9 in Polar Express's first
+    step) costs accuracy: measured 0.020-0.035 from the float64 polynomial
+    (Keller 0.015-0.017) where quintic_triton is at 0.010-0.016, so the bars are
+    0.05 and 0.03; a dropped or swapped term is off by more than 0.3."""
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(12))
+    for table, safety, fn, bar in ((dion_ref.POLAR_EXPRESS_COEFFICIENTS,
+                                    dion_ref.POLAR_EXPRESS_NORM_SAFETY, dion_ref.polar_express,
+                                    0.05),
+                                   (dion_ref.KELLER_COEFFICIENTS, dion_ref.KELLER_NORM_SAFETY,
+                                    dion_ref.keller, 0.03)):
+        wide = x if shape[-2] <= shape[-1] else x.mT
+        target = dion_ref.polynomial_float64(wide, table, safety)
+        if shape[-2] > shape[-1]:
+            target = target.mT
+        out = fn(x, 1e-7)
+        assert out.dtype == torch.bfloat16 and out.shape == x.shape
+        err = rel_fro(out.float(), target)
+        assert err < bar, (fn.__name__, shape, err)
+        if shape[-2] != shape[-1]:
+            flipped = fn(x.mT.contiguous(), 1e-7).mT
+            assert rel_fro(flipped.float(), out.float()) < 1e-2, (fn.__name__, shape)
 
 
 @pytest.mark.parametrize("shape", [(1, 256, 1024), (2, 64, 256)])
@@ -85,12 +143,12 @@ def test_keller_singular_values_in_band() -> None:
     assert float(s.min()) > 0.6 and float(s.max()) < 1.25
 
 
-def test_polar_express_vs_float64_polynomial() -> None:
+def test_polar_express_triton_vs_float64_polynomial() -> None:
     x = torch.randn(1, 128, 512, generator=torch.Generator().manual_seed(4))
     target = dion_ref.polynomial_float64(
         x, dion_ref.POLAR_EXPRESS_COEFFICIENTS, dion_ref.POLAR_EXPRESS_NORM_SAFETY
     )
-    assert rel_fro(dion_ref.polar_express(x, 1e-7).float(), target) < 0.03
+    assert rel_fro(dion_ref.polar_express_triton(x, 1e-7).float(), target) < 0.03
 
 
 def test_normalize_rows_closed_form() -> None:
@@ -127,6 +185,54 @@ def _float64_step(w, g, m, v, k, lr, mu, beta2, wd):
         w[b] *= 1 - lr * wd
         w[b, idx] += upd
     return w, m, v
+
+
+def _float64_muon_step(w, g, buf, v, lr, mu, beta2, wd, *, nesterov, normuon):
+    """Every-row steps written as Keller Jordan's Muon writes them
+    (tests/test_muon.py:104-115 of the reference): a momentum buffer
+    ``buf = mu buf + g``, the input ``g + mu buf`` (Nesterov) or ``buf``, the
+    exact polar factor, NorMuon or not, decoupled decay. Dion's state holds
+    ``M = mu buf``, so the two agree when ``buf`` starts at ``M / mu``."""
+    w, g, buf, v = (t.double().clone() for t in (w, g, buf, v))
+    blocks, rows, cols = w.shape
+    scale = lr * 0.2 * math.sqrt(max(rows, cols))
+    for b in range(blocks):
+        buf[b] = mu * buf[b] + g[b]
+        u = g[b] + mu * buf[b] if nesterov else buf[b]
+        o = dion_ref.exact_polar(u)
+        if normuon:
+            v[b] = v[b] + (1 - beta2) * ((o**2).mean(-1, keepdim=True) - v[b])
+            n = o / (v[b].sqrt() + 1e-8)
+            upd = n * (o.norm() / n.norm()) * -scale
+        else:
+            upd = o * -scale
+        w[b] *= 1 - lr * wd
+        w[b] += upd
+    return w, buf, v
+
+
+@pytest.mark.parametrize(("nesterov", "normuon"), [(False, True), (True, False), (False, False),
+                                                   (True, True)])
+def test_every_row_step_vs_float64_muon(nesterov: bool, normuon: bool) -> None:
+    """step_blocks with k = rows (heavy ball or Nesterov, NorMuon or none)
+    against the float64 Muon restatement, over three steps."""
+    g = torch.Generator().manual_seed(13)
+    w = torch.randn(2, 24, 40, generator=g) * 0.02
+    m = torch.zeros_like(w)
+    v = torch.zeros(2, 24, 1)
+    buf = torch.zeros_like(w)
+    w64, v64 = w.clone(), v.clone()
+    exact = lambda x, eps: dion_ref.exact_polar(x).float()  # noqa: E731
+    for _ in range(3):
+        grads = torch.randn(2, 24, 40, generator=g)
+        w64, buf, v64 = _float64_muon_step(w64, grads, buf, v64, 1e-3, 0.95, 0.95, 0.1,
+                                           nesterov=nesterov, normuon=normuon)
+        dion_ref.step_blocks(w, grads, m, v, k=24, lr=1e-3, mu=0.95, beta2=0.95, weight_decay=0.1,
+                             normuon=normuon, nesterov=nesterov, orthogonalize=exact)
+        assert rel_fro(m, 0.95 * buf) < 1e-6
+        assert rel_fro(w, w64) < 1e-6
+        if normuon:
+            assert rel_fro(v, v64) < 1e-5
 
 
 def test_step_blocks_vs_float64_restatement() -> None:
