@@ -249,14 +249,44 @@ def gram_ns_bench(torch, steps: int, warmup: int) -> dict:
     }
 
 
-def cpu_baseline(spec, fraction: float, threads: int) -> dict:
+def cpu_share() -> dict:
+    """The host CPUs this process may use: the affinity set, capped by a cgroup
+    CPU quota (a GPU box grants each job a share of a larger host), with the
+    host's own count and CPU model for the record."""
+    cpus = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else cpus
+    quota = None
+    try:
+        fields = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if fields and fields[0] != "max":
+            quota = max(1, int(int(fields[0]) // int(fields[1])))
+    except (OSError, ValueError, IndexError):
+        pass
+    if quota is not None:
+        usable = min(usable, quota)
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"threads": usable, "host_cpus": cpus, "cgroup_quota_cpus": quota, "cpu_model": model}
+
+
+def cpu_baseline(spec, fraction: float, share: dict) -> dict:
     """The CPU oracle on one decoder layer's Dion blocks plus 1/layers of the
-    AdamW elements, scaled by the layer count (labelled extrapolated)."""
+    AdamW elements, scaled by the layer count (labelled extrapolated): one
+    warm-up step, then the median of three timed steps, on every usable core."""
+    import statistics
+
     import numpy as np
     import torch
 
     from oracle import dion_ref
 
+    threads = share["threads"]
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     blocks = []
@@ -278,21 +308,49 @@ def cpu_baseline(spec, fraction: float, threads: int) -> dict:
         dion_ref.adamw(ap, ag, am, av, float(step), lr=3e-4, beta1=0.9, beta2=0.95,
                        weight_decay=0.05, eps=1e-8)
 
-    sample_layers = 3
     t0 = time.perf_counter()
-    for step in range(sample_layers):
-        one_layer(step + 1)
-    per_layer = (time.perf_counter() - t0) / sample_layers
+    one_layer(1)  # warm-up
+    samples = []
+    for step in range(2, 5):
+        t1 = time.perf_counter()
+        one_layer(step)
+        samples.append(time.perf_counter() - t1)
+    per_layer = statistics.median(samples)
     return {
         "value": per_layer * spec["layers"] * 1e3,
         "unit": "ms/step (extrapolated)",
         "cores": threads,
+        "host_cpus": share["host_cpus"],
+        "cgroup_quota_cpus": share["cgroup_quota_cpus"],
+        "cpu_model": share["cpu_model"],
         "kind": "port",
-        "sample": f"oracle (torch CPU restatement): one decoder layer's Dion blocks + "
-                  f"1/{spec['layers']} of the AdamW elements, stepped {sample_layers} times; "
-                  f"mean per layer x{spec['layers']} layers",
-        "sample_seconds": round(per_layer * sample_layers, 2),
+        "sample": f"oracle (torch CPU restatement, {threads} threads): one decoder layer's Dion "
+                  f"blocks + 1/{spec['layers']} of the AdamW elements; 1 warm-up step, median "
+                  f"of 3 steps, x{spec['layers']} layers",
+        "sample_seconds": round(time.perf_counter() - t0, 2),
     }
+
+
+# Busy-wait queued ahead of each dispatch sample: ~0.1 s at MI355X clocks, far
+# longer than a step's host work, so the host never waits on the GPU.
+GPU_BUSY_CYCLES = 200_000_000
+
+
+def host_dispatch_ms(torch, opt, samples: int = 7) -> float:
+    """Median host time of one ``opt.step()`` while the GPU is held busy
+    (reference bench/host_dispatch.py:28-56): the Python and launch overhead
+    alone, independent of how many steps are timed."""
+    import statistics
+
+    times = []
+    for _ in range(samples):
+        torch.cuda.synchronize()
+        torch.cuda._sleep(GPU_BUSY_CYCLES)
+        start = time.perf_counter()
+        opt.step()
+        times.append((time.perf_counter() - start) * 1e3)
+    torch.cuda.synchronize()
+    return statistics.median(times)
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
@@ -360,7 +418,7 @@ def probe() -> int:
     scores = torch.empty(18 * 14336, device=dev)
     rowsq = torch.empty_like(scores)
     _lib.call("dionw_accumulate_scores", _lib.ptr_array(grads), 18, 14336, 4096, mom.data_ptr(),
-              scores.data_ptr(), rowsq.data_ptr(), _lib.stream_handle(dev))
+              scores.data_ptr(), rowsq.data_ptr(), _lib.F16, _lib.stream_handle(dev))
     torch.cuda.synchronize()
     print("probe done: copy 1 GiB, grouped Newton-Schulz of the Llama-3-8B runs, "
           "accumulate 18x14336x4096")
@@ -421,14 +479,13 @@ def main() -> int:
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
-    host_t0 = time.perf_counter()
     start.record()
     for _ in range(args.steps):
         opt.step()
     end.record()
-    host_dispatch = (time.perf_counter() - host_t0) / args.steps * 1e3
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
+    host_dispatch = host_dispatch_ms(torch, opt)
 
     timeline = Timeline()
     timeline.wrap(_lib)
@@ -450,7 +507,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline and args.config == "llama3-8b":
         print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(spec, fraction, threads=min(os.cpu_count() or 1, 16))
+        cpu = cpu_baseline(spec, fraction, cpu_share())
 
     line = {
         "metric": {
