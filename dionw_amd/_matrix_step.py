@@ -56,7 +56,7 @@ from dionw_amd.newton_schulz import (
     run_newton_schulz_group,
 )
 
-__all__ = ["ACTIVE_RUNS", "MAX_RUN_ELEMENTS", "RunQueue", "run_elements", "step_run"]
+__all__ = ["ACTIVE_RUNS", "MAX_RUN_ELEMENTS", "RunQueue", "step_run"]
 
 # AdamW update RMS that matrix steps match (Moonshot's 0.2).
 ADAMW_UPDATE_RMS: Final[float] = 0.2
@@ -72,12 +72,6 @@ NEWTON_SCHULZ_EPS: Final[float] = 1e-8
 # the 256 CUs better (fewer partly idle tile rounds per product) and launch
 # fewer kernels; every Llama-3-8B bucket is one run.
 MAX_RUN_ELEMENTS: Final[int] = 2**30
-
-
-def run_elements(bucket: Bucket, position: int) -> int:
-    """Update elements of the parameter at ``position`` of ``bucket``."""
-    blocks = bucket.slices[position]
-    return (blocks.stop - blocks.start) * bucket.selected_rows * bucket.cols
 
 
 @dataclass

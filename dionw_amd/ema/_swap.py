@@ -1,84 +1,93 @@
-"""Temporary swaps of the live weights with their EMA shadows.
+"""Evaluation with the EMA weights: the live weights set aside and put back.
 
-Reference: src/dionw/ema/_swap.py:22-101.
+``WeightSwap`` holds the live values of the parameters whose shadows replaced
+them. Which parameters swap is decided by ``swap_plan``: every trainable
+parameter of the optimizer, or those of a given module, which must then share
+parameters with the optimizer and hold no trainable parameter outside it; the
+swap is all-or-nothing (every chosen parameter has a shadow, or none has:
+before the first update nothing is swapped). Behaviour and messages follow the
+reference (ema/_swap.py:22-101, ema/mixin.py:251-308).
 """
 
 from __future__ import annotations
 
-from collections.abc import Mapping, MutableMapping, Sequence
-from dataclasses import dataclass
+from collections.abc import Mapping, Sequence
 
 import torch
-from torch import Tensor
+from torch import Tensor, nn
 
 from dionw_amd.ema._keys import EMA_SHADOW
 
-__all__ = ["EmaSwapEntry", "collect_state_ema_swap_entries", "optimizer_managed_ema_swap_params"]
+__all__ = ["WeightSwap", "swap_plan"]
 
 
-@dataclass(frozen=True)
-class EmaSwapEntry:
-    """A parameter and its shadow."""
-
-    parameter: torch.nn.Parameter
-    shadow: Tensor
-
-
-def collect_state_ema_swap_entries(
-    *, params: Sequence[torch.nn.Parameter], optimizer_state: Mapping[Tensor, object], context: str
-) -> tuple[EmaSwapEntry, ...]:
-    """Every parameter's shadow, or nothing before the EMA has started.
+def swap_plan(model: nn.Module | None, managed: Sequence[nn.Parameter],
+              state: Mapping[Tensor, Mapping[str, object]], context: str
+              ) -> list[tuple[nn.Parameter, Tensor]]:
+    """The (parameter, shadow) pairs a swap applies; empty before any shadow.
 
     Raises:
-        ValueError: If ``params`` is empty.
+        ValueError: If there is nothing to swap, or ``model`` shares no
+            parameter with the optimizer or has trainable ones outside it.
         TypeError: If a shadow is not a tensor.
-        RuntimeError: If only some parameters have shadows.
+        RuntimeError: If only some of the chosen parameters have shadows.
     """
-    if not params:
+    if not managed:
         raise ValueError("No parameters available to swap with EMA weights")
-    found: list[EmaSwapEntry] = []
-    missing = 0
-    for parameter in params:
-        entry = optimizer_state.get(parameter)
-        shadow = entry.get(EMA_SHADOW) if isinstance(entry, MutableMapping) else None
+    chosen: Sequence[nn.Parameter] = managed
+    if model is not None:
+        ids = {id(p) for p in managed}
+        inside = [p for p in model.parameters() if id(p) in ids]
+        strangers = [p for p in model.parameters() if id(p) not in ids and p.requires_grad]
+        if strangers:
+            raise ValueError(f"{context} EMA swap received a model with {len(strangers)} "
+                             "trainable parameters outside the optimizer.")
+        if not inside:
+            raise ValueError(f"{context} EMA swap received a model with no optimizer-managed "
+                             "parameters.")
+        chosen = inside
+    pairs = []
+    for param in chosen:
+        shadow = state.get(param, {}).get(EMA_SHADOW)
         if shadow is None:
-            missing += 1
-        elif not isinstance(shadow, Tensor):
+            continue
+        if not isinstance(shadow, Tensor):
             raise TypeError(f"{context} EMA shadow must be a torch.Tensor")
-        else:
-            found.append(EmaSwapEntry(parameter, shadow))
-    if found and missing:
-        raise RuntimeError(
-            f"{context} EMA swap found {len(found)} initialized shadows for {len(params)} "
-            "parameters. Refusing to mix live and EMA weights."
-        )
-    return tuple(found)
+        pairs.append((param, shadow))
+    if pairs and len(pairs) != len(chosen):
+        raise RuntimeError(f"{context} EMA swap found {len(pairs)} initialized shadows for "
+                           f"{len(chosen)} parameters. Refusing to mix live and EMA weights.")
+    return pairs
 
 
-def optimizer_managed_ema_swap_params(
-    *,
-    model: torch.nn.Module | None,
-    optimizer_params: Sequence[torch.nn.Parameter],
-    context: str,
-) -> tuple[torch.nn.Parameter, ...]:
-    """The parameters to swap: the optimizer's, scoped to ``model`` if given.
+class WeightSwap:
+    """Live weights set aside while the EMA weights are in the parameters."""
 
-    Raises:
-        ValueError: Without optimizer parameters, or if ``model`` shares none
-            with the optimizer or has trainable parameters outside it.
-    """
-    if not optimizer_params:
-        raise ValueError("No parameters available to swap with EMA weights")
-    if model is None:
-        return tuple(optimizer_params)
-    managed = {id(p) for p in optimizer_params}
-    scoped = [p for p in model.parameters() if id(p) in managed]
-    outside = sum(1 for p in model.parameters() if id(p) not in managed and p.requires_grad)
-    if outside:
-        raise ValueError(
-            f"{context} EMA swap received a model with {outside} trainable parameters "
-            "outside the optimizer."
-        )
-    if not scoped:
-        raise ValueError(f"{context} EMA swap received a model with no optimizer-managed parameters.")
-    return tuple(scoped)
+    def __init__(self) -> None:
+        self._held: dict[int, tuple[nn.Parameter, Tensor]] = {}
+
+    @property
+    def active(self) -> bool:
+        """Whether EMA weights are in the parameters."""
+        return bool(self._held)
+
+    @torch.no_grad()
+    def apply(self, pairs: Sequence[tuple[nn.Parameter, Tensor]]) -> bool:
+        """Set the live weights aside and copy the shadows in.
+
+        Raises:
+            RuntimeError: If a swap is already active.
+        """
+        if self._held:
+            raise RuntimeError("EMA weights are already swapped in")
+        for param, shadow in pairs:
+            self._held[id(param)] = (param, param.data.clone())
+            param.data.copy_(shadow.to(device=param.device, dtype=param.dtype))
+        return bool(pairs)
+
+    @torch.no_grad()
+    def undo(self) -> None:
+        """Copy the live weights back."""
+        for param, live in self._held.values():
+            param.data.copy_(live)
+        self._held.clear()

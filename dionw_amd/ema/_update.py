@@ -1,10 +1,12 @@
 """EMA shadow arithmetic: ``lerp`` toward the live weights.
 
-Reference: src/dionw/ema/_update.py:17-70. GPU float32 sources update through
-the multi-tensor HIP kernel (one launch per 48 tensors, torch's lerp
-arithmetic, so a constant parameter keeps a bit-exact shadow); other sources
-are upcast into transient float32 copies a bounded chunk at a time; CPU
-shadows (CPU EMA) use torch's CPU lerp.
+Reference: src/dionw/ema/_update.py:17-70. Every GPU shadow updates through the
+multi-tensor HIP kernel (one launch per 48 tensors, torch's lerp arithmetic, so
+a constant parameter keeps a bit-exact shadow): a source of another dtype or
+layout is first copied into a float32 tensor laid out like the shadow, and a
+shadow that is not dense is updated in a dense copy that is copied back, a
+bounded chunk of such pairs at a time. CPU shadows (CPU EMA) are updated on
+the host with torch's CPU lerp, as the reference's CPU EMA does.
 """
 
 from __future__ import annotations
@@ -64,25 +66,31 @@ def foreach_ema_update_(shadows: list[Tensor], sources: list[Tensor], *, decay: 
     weight = 1.0 - decay
     direct_s: list[Tensor] = []
     direct_p: list[Tensor] = []
-    upcast: list[tuple[Tensor, Tensor]] = []
+    staged: list[tuple[Tensor, Tensor]] = []
     for shadow, source in zip(shadows, sources, strict=True):
-        if _kernel_ready(shadow, source):
+        if not shadow.is_cuda:
+            ema_update_(shadow, source.to(shadow.device, FP32), decay=decay)
+        elif shadow.shape != source.shape:
+            raise ValueError(f"EMA shadow {tuple(shadow.shape)} and source "
+                             f"{tuple(source.shape)} differ in shape")
+        elif _kernel_ready(shadow, source):
             direct_s.append(shadow)
             direct_p.append(source)
-        elif shadow.is_cuda and source.is_cuda and dense(shadow) and shadow.shape == source.shape:
-            upcast.append((shadow, source))
         else:
-            ema_update_(shadow, source.to(shadow.device, FP32), decay=decay)
+            staged.append((shadow, source))
     _hip_lerp(direct_s, direct_p, weight, copy=False)
     start = 0
-    while start < len(upcast):
-        stop, numel = start + 1, upcast[start][1].numel()
-        while stop < len(upcast) and numel + upcast[stop][1].numel() <= _STAGING_CHUNK_NUMEL:
-            numel += upcast[stop][1].numel()
+    while start < len(staged):
+        stop, numel = start + 1, staged[start][1].numel()
+        while stop < len(staged) and numel + staged[stop][1].numel() <= _STAGING_CHUNK_NUMEL:
+            numel += staged[stop][1].numel()
             stop += 1
-        chunk = upcast[start:stop]
-        staged = [torch.empty_like(shadow).copy_(source) for shadow, source in chunk]
-        _hip_lerp([s for s, _ in chunk], staged, weight, copy=False)
+        targets = [s if dense(s) else s.contiguous() for s, _ in staged[start:stop]]
+        inputs = [torch.empty_like(t).copy_(src) for t, (_, src) in zip(targets, staged[start:stop])]
+        _hip_lerp(targets, inputs, weight, copy=False)
+        for target, (shadow, _) in zip(targets, staged[start:stop]):
+            if target is not shadow:
+                shadow.copy_(target)
         start = stop
 
 

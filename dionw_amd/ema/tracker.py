@@ -1,264 +1,270 @@
-"""``OptimizerIntegratedEMA``: shadows in ``optimizer.state[p]``, GPU or CPU.
+"""``OptimizerIntegratedEMA``: EMA shadows kept in ``optimizer.state[p]``.
 
-Reference: src/dionw/ema/tracker.py:40-299. GPU shadows are queued during the
-step and updated at ``finalize_updates`` by the multi-tensor HIP kernels
-(copies for shadows not yet initialized, lerps for the rest), with no host
-synchronization; a Dion step may instead take the lerp of the parameters it
-writes into its own apply and AdamW passes (``fusable_shadows``), which then
-skip the queue. CPU shadows receive a snapshot copied on a side stream into
-pinned buffers, then a background thread applies the update (one job in
-flight at most).
+The schedule is a pure function of the step count (``cadence_at``). A due
+step updates every parameter's shadow after the optimizer's own update:
+
+- GPU shadows: each parameter queues a copy (first update, or a restart from
+  the live weights) or a lerp; ``finalize_updates`` runs each list as one
+  multi-tensor HIP launch per 48 tensors. The optimizer may instead take the
+  lerp inside its own pass over the new weights (``fusable_shadows``): a
+  parameter it marks as fused skips the queue.
+- CPU shadows: each parameter is copied into its pinned host buffer on a copy
+  stream, the training stream then waits for those copies on the GPU (no host
+  wait), and ``HostEmaWorker`` applies the batch on a background thread. The
+  next due step waits for that batch before reusing the buffers.
+
+The reference's tracker (ema/tracker.py:40-299) blocks the host on the
+previous copy at every step instead; the cadence and the arithmetic (lerp with
+``decay ** n``, a copy at the first update) are the same.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Any, Final
 
 import torch
 from torch import Tensor
 from torch.optim import Optimizer
 
-from dionw_amd.ema._cpu_job import AsyncCpuEmaItem, AsyncCpuEmaJob
+from dionw_amd.ema._host_worker import HostEmaWorker, HostSnapshot
 from dionw_amd.ema._keys import EMA_EVENT, EMA_INITIALIZED, EMA_PENDING, EMA_SHADOW, EMA_TMP_CPU
 from dionw_amd.ema._update import FP32, foreach_ema_copy_, foreach_ema_update_
 from dionw_amd.ema.config import EMAConfig, EMADevice, ProfileRegion
 
-__all__ = ["OptimizerIntegratedEMA", "new_cpu_staging"]
+__all__ = ["Cadence", "OptimizerIntegratedEMA", "cadence_at"]
 
 _STAGE_REGION: Final = "ema_stage_copy"
 _FINALIZE_REGION: Final = "ema_finalize"
 
 
-def new_cpu_staging(param: Tensor, *, pin: bool) -> Tensor:
-    """A zero CPU buffer for a parameter's snapshot (float32 and bfloat16 kept,
-    other dtypes staged as float32)."""
+@dataclass(frozen=True)
+class Cadence:
+    """What the EMA does at one optimizer step.
+
+    Attributes:
+        update: The shadows move this step.
+        from_live: Every shadow restarts as a copy of its parameter (the
+            configured ``start_step``).
+        decay: The lerp decay of a due update, ``decay_at_step ** n``; None
+            when nothing is lerped.
+    """
+
+    update: bool
+    from_live: bool
+    decay: float | None
+
+
+def cadence_at(config: EMAConfig, step_count: int) -> Cadence:
+    """The EMA's action at optimizer step ``step_count`` (1 for the first step).
+
+    With ``start_step = s > 0`` nothing happens before step s and step s copies
+    the live weights; after it (or from the start when s = 0) an update is due
+    every ``update_every_n_steps = n`` steps, lerping with the schedule's decay
+    raised to n so the half-life in steps does not depend on n
+    (reference tracker.py:154-175).
+    """
+    start, every = config.start_step, config.update_every_n_steps
+    if start > 0 and step_count < start:
+        return Cadence(False, False, None)
+    if start > 0 and step_count == start:
+        return Cadence(True, True, None)
+    since = step_count - start
+    if since <= 0 or since % every:
+        return Cadence(False, False, None)
+    return Cadence(True, False, config.decay_at_step(step_count) ** every)
+
+
+def _pinned_like(param: Tensor, *, pin: bool) -> Tensor:
+    """A zeroed host buffer for a parameter's snapshot (float32 and bfloat16
+    kept, other dtypes staged as float32)."""
     dtype = param.dtype if param.dtype in (FP32, torch.bfloat16) else FP32
     return torch.zeros_like(param, dtype=dtype, device="cpu", pin_memory=pin)
 
 
 class OptimizerIntegratedEMA:
-    """EMA shadows stored in an optimizer's per-parameter state."""
+    """EMA shadows stored in an optimizer's per-parameter state.
 
-    def __init__(self, optimizer: Optimizer, config: EMAConfig, profile_region: ProfileRegion) -> None:
+    Attributes:
+        optimizer: The optimizer whose state holds the shadows.
+        config: Schedule and placement.
+    """
+
+    def __init__(self, optimizer: Optimizer, config: EMAConfig,
+                 profile_region: ProfileRegion) -> None:
+        if config.device not in (EMADevice.GPU, EMADevice.CPU):
+            raise RuntimeError(f"Unhandled EMADevice: {config.device}")
         self.optimizer = optimizer
         self.config = config
-        self._profile_region = profile_region
-        if config.device is EMADevice.GPU:
-            self._use_gpu_shadow = True
-        elif config.device is EMADevice.CPU:
-            self._use_gpu_shadow = False
-        else:
-            raise RuntimeError(f"Unhandled EMADevice: {config.device}")
-        self._step_count = 0
-        self._do_update = True
-        self._initialize_from_live = False
-        self._eff_decay: float | None = None
-        self._cpu_ema_job: AsyncCpuEmaJob | None = None
-        self._cpu_fp32_staging: Tensor | None = None
+        self._region = profile_region
+        self._on_gpu = config.device is EMADevice.GPU
+        self._count = 0
+        self._now = Cadence(False, False, None)
+        self._copies: tuple[list[Tensor], list[Tensor]] = ([], [])
+        self._lerps: tuple[list[Tensor], list[Tensor]] = ([], [])
+        self._host = HostEmaWorker()
+        self._batch: list[HostSnapshot] = []
         self._copy_streams: dict[torch.device, torch.cuda.Stream] = {}
-        self._gpu_copy: tuple[list[Tensor], list[Tensor]] = ([], [])
-        self._gpu_lerp: tuple[list[Tensor], list[Tensor]] = ([], [])
-        # Parameters whose update of this step the optimizer's own pass took.
         self._fused: set[int] = set()
 
-    # -- schedule ------------------------------------------------------------
+    # -- schedule --------------------------------------------------------------
     @property
     def step_count(self) -> int:
         """Optimizer steps seen by the schedule (saved with the state)."""
-        return self._step_count
+        return self._count
 
     @step_count.setter
     def step_count(self, value: int) -> None:
         if value < 0:
-            raise ValueError(f"EMA step_count must be non-negative, got {value}")
-        self._step_count = value
+            raise ValueError(f"the EMA step count must be non-negative, got {value}")
+        self._count = value
 
     @property
     def uses_gpu_shadow(self) -> bool:
         """Whether shadows live on the parameters' GPU."""
-        return self._use_gpu_shadow
+        return self._on_gpu
 
     def begin_step(self) -> None:
-        """Advance the schedule at the start of an optimizer step."""
+        """Advance the schedule as an optimizer step starts."""
         self._fused.clear()
-        if not self._use_gpu_shadow:
-            self._wait_for_previous_snapshot_copy()
-        self._step_count += 1
-        n = self.config.update_every_n_steps
-        start = self.config.start_step
-        self._initialize_from_live = start > 0 and self._step_count == start
-        if start > 0 and self._step_count < start:
-            self._do_update = False
-        elif self._initialize_from_live:
-            self._do_update = True
-        else:
-            since = self._step_count - start
-            self._do_update = since > 0 and since % n == 0
-        decay = self.config.decay_at_step(self._step_count)
-        due_lerp = self._do_update and not self._initialize_from_live
-        self._eff_decay = decay**n if due_lerp else None
-        if self._do_update and not self._use_gpu_shadow:
-            self._wait_for_previous_cpu_update()
+        self._count += 1
+        self._now = cadence_at(self.config, self._count)
+        if self._now.update and not self._on_gpu:
+            self._host.wait()  # its host buffers are about to be refilled
 
     def should_update_this_step(self) -> bool:
-        """Whether this step updates the shadows."""
-        return self._do_update
+        """Whether this step moves the shadows."""
+        return self._now.update
 
-    # -- fusion into the optimizer's passes ------------------------------------
+    def _lerp_decay(self) -> float:
+        return self.config.decay if self._now.decay is None else self._now.decay
+
+    # -- fusion into the optimizer's own passes ----------------------------------
     def fusable_shadows(self, params: list[Tensor]) -> list[Tensor] | None:
-        """The shadows of ``params`` if this step's update of every one of them
-        is a GPU lerp that the optimizer may apply in its own pass over the new
-        weights (initialized float32 shadows laid out like their contiguous
-        float32 parameters), else None."""
-        if not (self._use_gpu_shadow and self._do_update) or self._initialize_from_live:
+        """The shadows of ``params`` when this step's update of every one of them
+        is a GPU lerp the optimizer may take in its pass over the new weights
+        (initialized float32 shadows laid out like their contiguous float32
+        parameters), else None."""
+        if not (self._on_gpu and self._now.update) or self._now.from_live:
             return None
         shadows = []
         for param in params:
-            state = self.optimizer.state.get(param)
-            shadow = state.get(EMA_SHADOW) if state else None
-            if (
-                shadow is None
-                or not state.get(EMA_INITIALIZED, False)
-                or param.dtype != FP32
-                or shadow.shape != param.shape
-                or shadow.device != param.device
-                or not (param.is_contiguous() and shadow.is_contiguous())
-            ):
+            entry = self.optimizer.state.get(param)
+            shadow = entry.get(EMA_SHADOW) if entry else None
+            if (shadow is None or not entry.get(EMA_INITIALIZED, False)
+                    or param.dtype is not FP32 or shadow.shape != param.shape
+                    or shadow.device != param.device
+                    or not (param.is_contiguous() and shadow.is_contiguous())):
                 return None
             shadows.append(shadow)
         return shadows
 
     def fused_weight(self) -> float:
-        """The lerp weight of this step's update (as foreach_ema_update_ forms it)."""
-        decay = self.config.decay if self._eff_decay is None else self._eff_decay
-        return 1.0 - decay
+        """The lerp weight ``1 - decay`` of this step's update."""
+        return 1.0 - self._lerp_decay()
 
     def mark_fused(self, params: list[Tensor]) -> None:
         """Record that the optimizer's pass updated these parameters' shadows."""
-        self._fused.update(id(param) for param in params)
+        self._fused.update(id(p) for p in params)
 
-    # -- queueing ------------------------------------------------------------
-    def _create_shadow(self, param: Tensor, state: dict[str, Any]) -> None:
-        if self._use_gpu_shadow and not param.is_cuda:
-            raise ValueError("EMA configured for the GPU but a parameter is on the CPU")
-        pin = self.config.pin_memory and not self._use_gpu_shadow
-        device = param.device if self._use_gpu_shadow else torch.device("cpu")
-        state[EMA_SHADOW] = torch.zeros_like(param, dtype=FP32, device=device, pin_memory=pin)
-        state[EMA_INITIALIZED] = False
-        if not self._use_gpu_shadow:
-            state[EMA_TMP_CPU] = new_cpu_staging(param, pin=pin)
+    # -- shadows -----------------------------------------------------------------
+    def _place(self, param: Tensor, entry: dict[str, Any], shadow: Tensor | None,
+               initialized: bool) -> None:
+        """Give ``param`` a float32 shadow on the EMA device (zeros, or a copy of
+        ``shadow``) and, for CPU EMA, its pinned staging buffer."""
+        if self._on_gpu and not param.is_cuda:
+            raise ValueError("the EMA is configured for the GPU but a parameter is on the CPU")
+        pin = self.config.pin_memory and not self._on_gpu
+        device = param.device if self._on_gpu else torch.device("cpu")
+        template = param if shadow is None else shadow
+        fresh = torch.zeros_like(template, dtype=FP32, device=device, pin_memory=pin)
+        if shadow is not None:
+            fresh.copy_(shadow)
+        entry[EMA_SHADOW] = fresh
+        entry[EMA_INITIALIZED] = initialized
+        entry[EMA_PENDING] = False
+        if not self._on_gpu:
+            entry[EMA_TMP_CPU] = _pinned_like(param, pin=pin)
+
+    def restore_shadow(self, param: Tensor, saved: Tensor, initialized: bool) -> None:
+        """Put a checkpoint's shadow of ``param`` on the EMA device.
+
+        Raises:
+            TypeError: If ``saved`` is not a tensor.
+        """
+        if not isinstance(saved, Tensor):
+            raise TypeError(f"{type(self.optimizer).__name__} EMA shadow must be a tensor")
+        self._place(param, self.optimizer.state[param], saved, bool(initialized))
 
     @torch.no_grad()
     def update_param(self, param: Tensor) -> None:
-        """Stage one parameter's update (parameters without state are skipped)."""
-        with self._profile_region(_STAGE_REGION):
-            if not self._do_update or param not in self.optimizer.state:
+        """Queue or stage one parameter's due update (parameters without
+        optimizer state are skipped)."""
+        with self._region(_STAGE_REGION):
+            if not self._now.update or param not in self.optimizer.state:
                 return
-            state = self.optimizer.state[param]
+            entry = self.optimizer.state[param]
             if id(param) in self._fused:
-                state[EMA_PENDING] = False
+                entry[EMA_PENDING] = False
                 return
-            if EMA_SHADOW not in state:
-                self._create_shadow(param, state)
-            if self._use_gpu_shadow:
-                if self._initialize_from_live or not state[EMA_INITIALIZED]:
-                    self._gpu_copy[0].append(state[EMA_SHADOW])
-                    self._gpu_copy[1].append(param)
-                    state[EMA_INITIALIZED] = True
-                else:
-                    self._gpu_lerp[0].append(state[EMA_SHADOW])
-                    self._gpu_lerp[1].append(param)
-                state[EMA_PENDING] = False
-            else:
-                self._stage_cpu_snapshot(param, state)
+            if EMA_SHADOW not in entry:
+                self._place(param, entry, None, False)
+            if not self._on_gpu:
+                self._stage(param, entry)
+                return
+            restart = self._now.from_live or not entry[EMA_INITIALIZED]
+            queue = self._copies if restart else self._lerps
+            queue[0].append(entry[EMA_SHADOW])
+            queue[1].append(param)
+            entry[EMA_INITIALIZED] = True
+            entry[EMA_PENDING] = False
 
-    def _copy_stream_for(self, device: torch.device) -> torch.cuda.Stream:
-        stream = self._copy_streams.get(device)
-        if stream is None:
-            stream = self._copy_streams[device] = torch.cuda.Stream(device=device)
-        return stream
-
-    def _stage_cpu_snapshot(self, param: Tensor, state: dict[str, Any]) -> None:
-        if self._initialize_from_live:
-            state[EMA_INITIALIZED] = False
-        tmp_cpu = state[EMA_TMP_CPU]
-        event = None
-        if param.is_cuda and tmp_cpu.is_pinned():
-            side = self._copy_stream_for(param.device)
-            side.wait_stream(torch.cuda.current_stream(param.device))
-            with torch.cuda.stream(side):
-                tmp_cpu.copy_(param, non_blocking=True)
-                event = torch.cuda.Event(blocking=False)
-                event.record(side)
+    def _stage(self, param: Tensor, entry: dict[str, Any]) -> None:
+        if self._now.from_live:
+            entry[EMA_INITIALIZED] = False
+        staged = entry[EMA_TMP_CPU]
+        ready = None
+        if param.is_cuda and staged.is_pinned():
+            stream = self._copy_streams.get(param.device)
+            if stream is None:
+                stream = self._copy_streams[param.device] = torch.cuda.Stream(param.device)
+            stream.wait_stream(torch.cuda.current_stream(param.device))
+            with torch.cuda.stream(stream):
+                staged.copy_(param, non_blocking=True)
+                ready = torch.cuda.Event()
+                ready.record(stream)
         else:
-            tmp_cpu.copy_(param, non_blocking=False)
-        state[EMA_EVENT] = event
-        state[EMA_PENDING] = True
+            staged.copy_(param)
+        entry[EMA_EVENT] = ready
+        entry[EMA_PENDING] = True
+        self._batch.append(HostSnapshot(entry, ready, entry[EMA_SHADOW], staged))
 
-    # -- applying ------------------------------------------------------------
     @torch.no_grad()
-    def _finalize_gpu_updates(self) -> None:
-        if self._gpu_copy[0]:
-            foreach_ema_copy_(*self._gpu_copy)
-            self._gpu_copy[0].clear()
-            self._gpu_copy[1].clear()
-        if self._gpu_lerp[0]:
-            decay = self.config.decay if self._eff_decay is None else self._eff_decay
-            foreach_ema_update_(*self._gpu_lerp, decay=decay)
-            self._gpu_lerp[0].clear()
-            self._gpu_lerp[1].clear()
+    def _run_device_queues(self) -> None:
+        if self._copies[0]:
+            foreach_ema_copy_(*self._copies)
+        if self._lerps[0]:
+            foreach_ema_update_(*self._lerps, decay=self._lerp_decay())
+        for queue in (self._copies, self._lerps):
+            queue[0].clear()
+            queue[1].clear()
 
     @torch.no_grad()
     def finalize_updates(self) -> None:
-        """Apply this step's GPU updates, or start the CPU worker on them."""
-        with self._profile_region(_FINALIZE_REGION):
-            if self._use_gpu_shadow:
-                self._finalize_gpu_updates()
+        """Apply this step's GPU updates, or hand the staged batch to the host
+        worker."""
+        with self._region(_FINALIZE_REGION):
+            if self._on_gpu:
+                self._run_device_queues()
                 self._fused.clear()
                 return
-            if not self._do_update:
+            batch, self._batch = self._batch, []
+            if not batch:
                 return
-            decay = self.config.decay if self._eff_decay is None else self._eff_decay
-            items = []
-            for group in self.optimizer.param_groups:
-                for param in group["params"]:
-                    state = self.optimizer.state.get(param)
-                    if state and state.get(EMA_PENDING, False):
-                        items.append(
-                            AsyncCpuEmaItem(state, state[EMA_EVENT], state[EMA_SHADOW],
-                                            state[EMA_TMP_CPU])
-                        )
-            if not items:
-                return
-            if self._cpu_ema_job is not None:
-                raise RuntimeError("CPU EMA job already pending after the pre-step wait")
-            job = AsyncCpuEmaJob(items=items, decay=decay, fp32_staging=self._staging_for(items))
-            self._cpu_ema_job = job
-            job.start()
-
-    def _staging_for(self, items: list[AsyncCpuEmaItem]) -> Tensor | None:
-        need = max((i.tmp_cpu.numel() for i in items if i.tmp_cpu.dtype != FP32), default=0)
-        if need == 0:
-            return None
-        if self._cpu_fp32_staging is None or self._cpu_fp32_staging.numel() < need:
-            self._cpu_fp32_staging = torch.empty(need, dtype=FP32, device="cpu")
-        return self._cpu_fp32_staging
-
-    # -- waiting ---------------------------------------------------------------
-    def _wait_for_previous_snapshot_copy(self) -> None:
-        job = self._cpu_ema_job
-        if job is None:
-            return
-        job.wait_for_copy()
-        if job.done():
-            job.wait_for_update()
-            self._cpu_ema_job = None
-
-    def _wait_for_previous_cpu_update(self) -> None:
-        job = self._cpu_ema_job
-        if job is not None:
-            job.wait_for_update()
-            self._cpu_ema_job = None
+            # Later writes of the parameters wait for the copies on the GPU.
+            for device, stream in self._copy_streams.items():
+                torch.cuda.current_stream(device).wait_stream(stream)
+            self._host.submit(batch, self._lerp_decay())
 
     def flush_pending_updates(self) -> None:
         """Finish queued EMA work before the shadows are read.
@@ -266,7 +272,7 @@ class OptimizerIntegratedEMA:
         Raises:
             RuntimeError: If the CPU worker failed.
         """
-        if self._use_gpu_shadow:
-            self._finalize_gpu_updates()
+        if self._on_gpu:
+            self._run_device_queues()
         else:
-            self._wait_for_previous_cpu_update()
+            self._host.wait()

@@ -1,12 +1,16 @@
-"""``param_groups(model)``: route every parameter and build Dion param groups.
+"""``param_groups(model)``: route every trainable parameter and build Dion groups.
 
-Reference: src/dionw/param_groups.py:89-270. A declared route wins (a
-``RouteProvider`` module's ``dion_routes`` or the ``routes`` argument;
-conflicting declarations raise); other parameters follow the default rule.
-A matrix block takes ``fraction`` of its rows per step when its smaller side is
-at least ``selection_min_dim``, every row otherwise. Decayed groups carry no
-``weight_decay`` key (they take the optimizer's); exempt groups carry 0.0.
-AdamW groups come first, then matrix groups, each in parameter order.
+A ``_Router`` indexes the model once (where each parameter is registered, the
+routes its ``RouteProvider`` modules and the ``routes`` argument declare) and
+decides each parameter: a declared route wins over the default rule table
+(``_routing_rules``); a MATRIX parameter takes ``fraction`` of its blocks'
+rows per step when the blocks' smaller side is at least ``selection_min_dim``,
+every row otherwise, unless its route fixes the fraction. The decisions are
+then laid out as groups — AdamW groups first, then matrix groups, each group
+one combination of (route, heads, fraction, decay) in order of first
+appearance, parameters in their given order. Decayed groups carry no
+``weight_decay`` (they take the optimizer's), exempt ones carry 0.0. The
+outcome and the error messages are the reference's (param_groups.py:89-270).
 """
 
 from __future__ import annotations
@@ -17,15 +21,15 @@ from typing import Any, NamedTuple
 
 from torch import Tensor, nn
 
-from dionw_amd._buckets import block_shape
-from dionw_amd._default_rule import Owner, default_route, is_exempt_from_decay, owners
+from dionw_amd._groups import matrix_blocks
 from dionw_amd._keys import FRACTION_KEY, NUM_HEADS_KEY, ROUTE_KEY
+from dionw_amd._routing_rules import Site, decay_exempt, default_route, sites
 from dionw_amd.report import RoutedParameter, RouteReason, RoutingReport
 from dionw_amd.routing import Route, RouteKind, RouteProvider
 
 __all__ = ["ROUTE_KEY", "ParamGroups", "param_groups"]
 
-_LOGGER = logging.getLogger("dionw")
+_LOG = logging.getLogger("dionw")
 
 
 class ParamGroups(NamedTuple):
@@ -33,6 +37,92 @@ class ParamGroups(NamedTuple):
 
     groups: list[dict[str, Any]]
     report: RoutingReport
+
+
+class _Router:
+    """Routes the parameters of one model under one set of settings."""
+
+    def __init__(self, model: nn.Module, *, fraction: float, selection_min_dim: int,
+                 min_matrix_dim: int, routes: Mapping[Tensor, Route] | None) -> None:
+        if not 0.0 < fraction <= 1.0:
+            raise ValueError(f"fraction must be in (0, 1], got {fraction}")
+        if selection_min_dim <= 0 or min_matrix_dim <= 0:
+            raise ValueError("selection_min_dim and min_matrix_dim must be positive")
+        self.fraction = fraction
+        self.selection_min_dim = selection_min_dim
+        self.min_matrix_dim = min_matrix_dim
+        self.sites = sites(model)
+        self.declared = self._collect_declarations(model, routes)
+
+    def _collect_declarations(self, model: nn.Module,
+                              routes: Mapping[Tensor, Route] | None) -> dict[int, Route]:
+        """Declared routes by parameter id; a declaration must name a parameter
+        of the model, and two declarations of one parameter must agree."""
+        claims: list[tuple[str, Tensor, Route]] = [
+            ("the routes argument", param, route) for param, route in (routes or {}).items()]
+        for module in model.modules():
+            if isinstance(module, RouteProvider):
+                claims += [(type(module).__name__, p, r) for p, r in module.dion_routes()]
+        declared: dict[int, Route] = {}
+        for source, param, route in claims:
+            if id(param) not in self.sites:
+                raise ValueError(f"{source} declares a route for a parameter (shape "
+                                 f"{tuple(param.shape)}) that is not registered on the model")
+            known = declared.get(id(param))
+            if known is not None and known != route:
+                raise ValueError(f"Conflicting routes for a parameter of shape "
+                                 f"{tuple(param.shape)}: {known} vs {route} ({source})")
+            declared[id(param)] = route
+        return declared
+
+    def decide(self, param: Tensor, decayed: bool) -> RoutedParameter:
+        """One parameter's route, row fraction, head split and decay."""
+        site: Site = self.sites[id(param)]
+        route = self.declared.get(id(param))
+        if route is None:
+            route, reason = default_route(site, param, self.min_matrix_dim)
+        else:
+            reason = RouteReason.DECLARED
+        if route.kind is RouteKind.ADAMW:
+            rows_fraction = 1.0
+        elif route.kind is RouteKind.MATRIX:
+            if param.ndim < 2:
+                raise ValueError(f"MATRIX route on {site.path} needs >= 2 dims, got "
+                                 f"{tuple(param.shape)}")
+            _, rows, cols = matrix_blocks(param, route.num_heads)
+            if route.fraction is not None:
+                rows_fraction = float(route.fraction)
+            elif min(rows, cols) >= self.selection_min_dim:
+                rows_fraction = self.fraction
+            else:
+                rows_fraction = 1.0
+        else:
+            raise RuntimeError(f"Unhandled RouteKind: {route.kind}")
+        return RoutedParameter(name=site.path, shape=tuple(int(d) for d in param.shape),
+                               kind=route.kind, fraction=rows_fraction,
+                               num_heads=route.num_heads, decayed=decayed, reason=reason)
+
+
+def _layout(params: list[Tensor], decisions: list[RoutedParameter]) -> ParamGroups:
+    """Groups (AdamW first, then MATRIX; each by first appearance) and the
+    report in the same order."""
+    slots: dict[tuple[Any, ...], list[int]] = {}
+    for i, d in enumerate(decisions):
+        slots.setdefault((d.kind is RouteKind.MATRIX, d.kind, d.num_heads, d.fraction,
+                          d.decayed), []).append(i)
+    groups: list[dict[str, Any]] = []
+    order: list[int] = []
+    for key in sorted(slots, key=lambda k: k[0]):  # stable: first appearance within a kind
+        members = slots[key]
+        _, kind, num_heads, fraction, decayed = key
+        group: dict[str, Any] = {"params": [params[i] for i in members], ROUTE_KEY: kind.value}
+        if kind is RouteKind.MATRIX:
+            group.update({FRACTION_KEY: fraction, NUM_HEADS_KEY: num_heads})
+        if not decayed:
+            group["weight_decay"] = 0.0
+        groups.append(group)
+        order += members
+    return ParamGroups(groups, RoutingReport(tuple(decisions[i] for i in order)))
 
 
 def param_groups(
@@ -47,127 +137,37 @@ def param_groups(
 ) -> ParamGroups:
     """Route each trainable parameter of ``model`` and build ``Dion`` groups.
 
+    Args:
+        model: Owns the parameters; its ``RouteProvider`` modules declare routes.
+        params: The parameters to optimize (None: all of ``model``'s); those
+            without ``requires_grad`` are skipped.
+        fraction: Row fraction of blocks whose smaller side is at least
+            ``selection_min_dim``, in (0, 1].
+        selection_min_dim: Smaller side from which blocks select rows.
+        min_matrix_dim: Smaller side below which tensors take AdamW.
+        routes: Extra per-parameter routes, merged with the modules' own.
+        no_weight_decay: Exactly the parameters exempt from weight decay (None:
+            the default rule).
+
+    Returns:
+        ``(groups, report)``; the report is also logged at INFO on ``dionw``.
+
     Raises:
-        ValueError: On out-of-range settings, invalid or conflicting routes,
+        ValueError: For out-of-range settings, invalid or conflicting routes,
             parameters not registered on ``model``, or nothing trainable.
     """
-    if not 0.0 < fraction <= 1.0:
-        raise ValueError(f"fraction must be in (0, 1], got {fraction}")
-    if selection_min_dim <= 0 or min_matrix_dim <= 0:
-        raise ValueError("selection_min_dim and min_matrix_dim must be positive")
-    found = owners(model)
-    trainable: dict[int, Tensor] = {}
-    for param in model.parameters() if params is None else params:
-        if param.requires_grad and id(param) not in trainable:
-            trainable[id(param)] = param
-    if not trainable:
+    router = _Router(model, fraction=fraction, selection_min_dim=selection_min_dim,
+                     min_matrix_dim=min_matrix_dim, routes=routes)
+    chosen = list({id(p): p for p in (model.parameters() if params is None else params)
+                   if p.requires_grad}.values())
+    if not chosen:
         raise ValueError("No parameters require gradients")
-    foreign = [tuple(p.shape) for key, p in trainable.items() if key not in found]
-    if foreign:
-        raise ValueError(f"Parameters not registered on the model: {foreign[:8]}")
-    if no_weight_decay is None:
-        exempt = {key for key, p in trainable.items() if is_exempt_from_decay(found[key], p)}
-    else:
-        exempt = {id(p) for p in no_weight_decay}
-    declared = _declarations(model, routes)
-    routed = [
-        _resolve(
-            found[key],
-            param,
-            declared.get(key),
-            fraction,
-            selection_min_dim,
-            min_matrix_dim,
-            decayed=key not in exempt,
-        )
-        for key, param in trainable.items()
-    ]
-    groups, report = _groups(list(trainable.values()), routed)
-    _LOGGER.info("\n".join(report.lines()))
-    return ParamGroups(groups=groups, report=report)
-
-
-def _declarations(model: nn.Module, routes: Mapping[Tensor, Route] | None) -> dict[int, Route]:
-    sources: list[tuple[str, Tensor, Route]] = [
-        ("the routes argument", p, r) for p, r in (routes or {}).items()
-    ]
-    for module in model.modules():
-        if isinstance(module, RouteProvider):
-            sources.extend((type(module).__name__, p, r) for p, r in module.dion_routes())
-    registered = {id(p) for p in model.parameters()}
-    declared: dict[int, Route] = {}
-    for source, param, route in sources:
-        if id(param) not in registered:
-            raise ValueError(
-                f"{source} declares a route for a parameter (shape {tuple(param.shape)}) "
-                "that is not registered on the model"
-            )
-        earlier = declared.setdefault(id(param), route)
-        if earlier != route:
-            raise ValueError(
-                f"Conflicting routes for a parameter of shape {tuple(param.shape)}: "
-                f"{earlier} vs {route} ({source})"
-            )
-    return declared
-
-
-def _resolve(
-    owner: Owner,
-    param: Tensor,
-    declared: Route | None,
-    fraction: float,
-    selection_min_dim: int,
-    min_matrix_dim: int,
-    *,
-    decayed: bool,
-) -> RoutedParameter:
-    if declared is None:
-        route, reason = default_route(owner, param, min_matrix_dim)
-    else:
-        route, reason = declared, RouteReason.DECLARED
-    if route.kind is RouteKind.MATRIX:
-        if param.ndim < 2:
-            raise ValueError(
-                f"MATRIX route on {owner.name} needs >= 2 dims, got {tuple(param.shape)}"
-            )
-        _, rows, cols = block_shape(param, route.num_heads)
-        if route.fraction is not None:
-            row_fraction = float(route.fraction)
-        else:
-            row_fraction = fraction if min(rows, cols) >= selection_min_dim else 1.0
-    elif route.kind is RouteKind.ADAMW:
-        row_fraction = 1.0
-    else:
-        raise RuntimeError(f"Unhandled RouteKind: {route.kind}")
-    return RoutedParameter(
-        name=owner.name,
-        shape=tuple(int(d) for d in param.shape),
-        kind=route.kind,
-        fraction=row_fraction,
-        num_heads=route.num_heads,
-        decayed=decayed,
-        reason=reason,
-    )
-
-
-def _groups(
-    params: list[Tensor], routed: list[RoutedParameter]
-) -> tuple[list[dict[str, Any]], RoutingReport]:
-    buckets: dict[tuple[RouteKind, int | None, float, bool], list[int]] = {}
-    for position, entry in enumerate(routed):
-        key = (entry.kind, entry.num_heads, entry.fraction, entry.decayed)
-        buckets.setdefault(key, []).append(position)
-    # AdamW groups first; within a kind, first-seen order (a stable sort).
-    ordered = sorted(buckets.items(), key=lambda item: item[0][0] is RouteKind.MATRIX)
-    groups: list[dict[str, Any]] = []
-    entries: list[RoutedParameter] = []
-    for (kind, num_heads, row_fraction, decayed), positions in ordered:
-        group: dict[str, Any] = {"params": [params[i] for i in positions], ROUTE_KEY: kind.value}
-        if kind is RouteKind.MATRIX:
-            group[FRACTION_KEY] = row_fraction
-            group[NUM_HEADS_KEY] = num_heads
-        if not decayed:
-            group["weight_decay"] = 0.0
-        groups.append(group)
-        entries.extend(routed[i] for i in positions)
-    return groups, RoutingReport(tuple(entries))
+    outside = [tuple(p.shape) for p in chosen if id(p) not in router.sites]
+    if outside:
+        raise ValueError(f"Parameters not registered on the model: {outside[:8]}")
+    exempt = ({id(p) for p in chosen if decay_exempt(router.sites[id(p)], p)}
+              if no_weight_decay is None else {id(p) for p in no_weight_decay})
+    decisions = [router.decide(p, id(p) not in exempt) for p in chosen]
+    result = _layout(chosen, decisions)
+    _LOG.info("\n".join(result.report.lines()))
+    return result

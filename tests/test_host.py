@@ -20,7 +20,7 @@ from torch import nn
 import dionw_amd
 from dionw_amd import EMAConfig, Route, RouteKind, RouteReason, param_groups
 from dionw_amd import _lib
-from dionw_amd.optimizer import _check_structure, _with_pre_option_keys
+from dionw_amd._groups import refuse_structural_change
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "dionw_hip.h"
 
@@ -301,8 +301,17 @@ def test_structural_key_refusal() -> None:
                 "newton_schulz": "gram", "row_normalization": "normuon",
                 "momentum_form": "heavy_ball"}]
     with pytest.raises(ValueError, match="'fraction'"):
-        _check_structure(_with_pre_option_keys(saved), current)
+        refuse_structural_change(saved, current)
     current[0]["fraction"] = 0.25
-    _check_structure(_with_pre_option_keys(saved), current)
+    completed = refuse_structural_change(saved, current)
+    # a checkpoint from before the update options is NorMuon with heavy-ball momentum
+    assert completed[0]["row_normalization"] == "normuon"
+    assert completed[0]["momentum_form"] == "heavy_ball"
+    current[0]["momentum_form"] = "nesterov"
+    with pytest.raises(ValueError, match="'momentum_form'"):
+        refuse_structural_change(saved, current)
     with pytest.raises(ValueError, match="param groups"):
-        _check_structure(saved, current * 2)
+        refuse_structural_change(saved, current * 2)
+    with pytest.raises(ValueError, match="'newton_schulz'"):
+        refuse_structural_change([{"dion_route": "matrix", "fraction": 0.25, "num_heads": None}],
+                                 current)

@@ -1,0 +1,180 @@
+"""Host logic of the optimizer and the EMA that needs no GPU.
+
+Run splitting (reference tests/test_optimizer.py:688-730), the EMA cadence
+(tests/test_ema.py:141-205), the CPU EMA worker's error path
+(ema/_cpu_job.py:36-43, 104-137), swap planning (tests/test_ema.py:320-362),
+group validation messages (tests/test_optimizer.py:455-480, 740-798) and the
+scratch-buffer keying.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch import nn
+
+from dionw_amd import _workspace
+from dionw_amd import optimizer as opt_module
+from dionw_amd._buckets import Bucket
+from dionw_amd._groups import GroupSpec, check_decays, check_parameter, matrix_blocks
+from dionw_amd.ema import EMAConfig
+from dionw_amd.ema._host_worker import HostEmaWorker, HostSnapshot
+from dionw_amd.ema._keys import EMA_INITIALIZED, EMA_PENDING
+from dionw_amd.ema._swap import WeightSwap, swap_plan
+from dionw_amd.ema.tracker import cadence_at
+
+
+def _bucket(block_counts: list[int], grads: list[bool], rows: int = 32, cols: int = 48,
+            selected: int = 32) -> Bucket:
+    params = []
+    for count, has_grad in zip(block_counts, grads):
+        p = nn.Parameter(torch.zeros(count * rows, cols))
+        p.grad = torch.zeros_like(p) if has_grad else None
+        params.append(p)
+    offsets = [0]
+    for count in block_counts:
+        offsets.append(offsets[-1] + count)
+    n = offsets[-1]
+    return Bucket(0, lambda x, e: x, params, offsets, rows, cols, selected,
+                  torch.zeros(n, rows, cols), torch.zeros(n, rows, 1))
+
+
+def test_runs_split_at_missing_gradients_and_the_cap(monkeypatch) -> None:
+    bucket = _bucket([1, 1, 1, 1, 1], [True, True, False, True, True])
+    assert list(opt_module._runs(bucket)) == [[0, 1], [3, 4]]
+    monkeypatch.setattr(opt_module, "MAX_RUN_ELEMENTS", 2 * 32 * 48)
+    four = _bucket([1, 1, 1, 1], [True] * 4)
+    assert list(opt_module._runs(four)) == [[0, 1], [2, 3]]
+    # a parameter larger than the cap runs alone; selected rows count, not rows
+    big = _bucket([3, 1, 1], [True] * 3, selected=8)
+    monkeypatch.setattr(opt_module, "MAX_RUN_ELEMENTS", 2 * 8 * 48)
+    assert list(opt_module._runs(big)) == [[0], [1, 2]]
+    assert list(opt_module._runs(_bucket([1, 1], [False, False]))) == []
+
+
+def test_bucket_block_ranges_and_views() -> None:
+    bucket = _bucket([2, 1, 3], [True] * 3)
+    assert bucket.blocks_per_param == 2
+    assert bucket.param_blocks(2) == slice(3, 6)
+    assert bucket.run_blocks([1, 2]) == slice(2, 6)
+    state: dict = {bucket.params[1]: {"momentum": torch.ones(32, 48)}}
+    state.setdefault(bucket.params[0], {})
+    state.setdefault(bucket.params[2], {})
+    bucket.adopt(state)
+    assert torch.equal(bucket.momentum[2], torch.ones(32, 48))  # an existing entry is copied in
+    assert state[bucket.params[2]]["momentum"].untyped_storage().data_ptr() == \
+        bucket.momentum.untyped_storage().data_ptr()
+    assert state[bucket.params[2]]["variance"].shape == (96, 1)
+
+
+def test_matrix_blocks() -> None:
+    assert matrix_blocks(torch.zeros(64, 3, 3, 8), None) == (1, 64, 72)
+    assert matrix_blocks(torch.zeros(96, 16), 3) == (3, 32, 16)
+    with pytest.raises(ValueError, match="does not divide"):
+        matrix_blocks(torch.zeros(30, 16), 4)
+
+
+def test_ema_cadence_table() -> None:
+    every2 = EMAConfig(decay=0.9, update_every_n_steps=2)
+    table = [cadence_at(every2, n) for n in range(1, 6)]
+    assert [c.update for c in table] == [False, True, False, True, False]
+    assert table[1].decay == pytest.approx(0.81) and not table[1].from_live
+    delayed = EMAConfig(decay=0.9, update_every_n_steps=2, start_step=3)
+    table = [cadence_at(delayed, n) for n in range(1, 8)]
+    assert [c.update for c in table] == [False, False, True, False, True, False, True]
+    assert table[2].from_live and table[2].decay is None
+    ramp = EMAConfig(decay=0.9, decay_final=0.99, decay_ramp_steps=10)
+    assert cadence_at(ramp, 5).decay == pytest.approx(0.945)
+    power = EMAConfig(decay=0.999, power_gamma=1.0)
+    assert cadence_at(power, 2).decay == pytest.approx(0.25)
+
+
+def test_host_worker_rejects_device_buffers_and_reraises_failures() -> None:
+    entry = {EMA_INITIALIZED: True, EMA_PENDING: True}
+    with pytest.raises(ValueError, match="must live on the CPU"):
+        HostSnapshot(entry, None, torch.zeros(4), torch.zeros(4, device="meta"))
+    worker = HostEmaWorker()
+    bad = HostSnapshot(entry, None, torch.zeros(4), torch.zeros(5))  # shapes disagree
+    worker.submit([bad], decay=0.9)
+    with pytest.raises(RuntimeError, match="CPU EMA update failed"):
+        worker.wait()
+    worker.wait()  # the failure is reported once
+    shadow, staged = torch.zeros(4), torch.full((4,), 2.0)
+    good = {EMA_INITIALIZED: False, EMA_PENDING: True}
+    worker.submit([HostSnapshot(good, None, shadow, staged)], decay=0.9)
+    worker.wait()
+    assert torch.equal(shadow, staged) and good[EMA_INITIALIZED] and not good[EMA_PENDING]
+    worker.submit([HostSnapshot(good, None, shadow, torch.zeros(4, dtype=torch.bfloat16))],
+                  decay=0.5)
+    worker.wait()
+    assert torch.equal(shadow, torch.ones(4))  # lerp through the float32 scratch
+
+
+def test_swap_plan_and_weight_swap() -> None:
+    a, b = nn.Parameter(torch.ones(3)), nn.Parameter(torch.ones(2))
+    state = {a: {"ema_shadow": torch.zeros(3)}, b: {"ema_shadow": torch.full((2,), 5.0)}}
+    pairs = swap_plan(None, [a, b], state, "Dion")
+    swap = WeightSwap()
+    assert swap.apply(pairs) and swap.active
+    assert torch.equal(a.data, torch.zeros(3))
+    with pytest.raises(RuntimeError, match="already swapped"):
+        swap.apply(pairs)
+    swap.undo()
+    assert not swap.active and torch.equal(a.data, torch.ones(3))
+    assert swap_plan(None, [a], {}, "Dion") == []  # before the first update
+    with pytest.raises(RuntimeError, match="Refusing to mix"):
+        swap_plan(None, [a, b], {a: state[a]}, "Dion")
+    with pytest.raises(ValueError, match="outside the optimizer"):
+        swap_plan(nn.Linear(2, 2), [a, b], state, "Dion")
+    with pytest.raises(ValueError, match="no optimizer-managed parameters"):
+        swap_plan(nn.Linear(2, 2).requires_grad_(False), [a, b], state, "Dion")
+    with pytest.raises(ValueError, match="No parameters"):
+        swap_plan(None, [], state, "Dion")
+
+
+def _group(**extra) -> dict:
+    base = {"params": [torch.zeros(8, 8)], "lr": 1e-3, "weight_decay": 0.0, "fraction": 1.0,
+            "num_heads": None, "newton_schulz": "gram", "row_normalization": "normuon",
+            "momentum_form": "heavy_ball", "dion_route": "matrix"}
+    base.update(extra)
+    return base
+
+
+def test_group_spec_messages() -> None:
+    spec = GroupSpec.of(_group(fraction=0.5))
+    assert spec.fraction == 0.5 and spec.num_heads is None
+    no_route = _group()
+    del no_route["dion_route"]
+    with pytest.raises(TypeError, match=r"dionw\.param_groups"):
+        GroupSpec.of(no_route)
+    with pytest.raises(ValueError, match="fraction"):
+        GroupSpec.of(_group(fraction=1.5))
+    with pytest.raises(ValueError, match="Nesterov momentum needs every row"):
+        GroupSpec.of(_group(fraction=0.5, momentum_form="nesterov"))
+    with pytest.raises(ValueError, match="route it to AdamW"):
+        GroupSpec.of(_group(params=[torch.zeros(8)]))
+    with pytest.raises(ValueError, match="does not divide"):
+        GroupSpec.of(_group(params=[torch.zeros(30, 16)], num_heads=4))
+    with pytest.raises(ValueError, match="lr and weight_decay"):
+        GroupSpec.of(_group(lr=-1.0))
+    with pytest.raises(ValueError, match="'row_normalization'|is not a valid"):
+        GroupSpec.of(_group(row_normalization="bogus"))
+    with pytest.raises(ValueError, match="momentum"):
+        check_decays(lr=1.0, weight_decay=0.0, eps=1e-8, decays={"momentum": 1.0})
+    with pytest.raises(ValueError, match="lr and weight_decay"):
+        check_decays(lr=1.0, weight_decay=0.0, eps=0.0, decays={})
+    with pytest.raises(ValueError, match="CUDA"):
+        check_parameter(torch.zeros(2, 2))
+
+
+def test_workspace_is_keyed_by_device_and_stream() -> None:
+    cpu = torch.device("cpu")
+    _workspace.release(cpu)
+    a = _workspace.buffer(cpu, "t", (4,), torch.float32, stream=1)
+    b = _workspace.buffer(cpu, "t", (4,), torch.float32, stream=2)
+    assert a.data_ptr() != b.data_ptr()
+    assert _workspace.buffer(cpu, "t", (2,), torch.float32, stream=1).data_ptr() == a.data_ptr()
+    grown = _workspace.buffer(cpu, "t", (1000,), torch.float32, stream=1)
+    assert grown.numel() == 1000 and _workspace.held_bytes(cpu) >= 4000
+    _workspace.release(cpu)
+    assert _workspace.held_bytes(cpu) == 0
