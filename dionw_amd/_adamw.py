@@ -86,3 +86,5 @@ def adamw_step(group: dict[str, Any], state: ParamState) -> None:
     for original, copy in copies:
         if original.data_ptr() != copy.data_ptr():
             original.copy_(copy)
+    if ema is not None:
+        ema.stage_written(params)

@@ -317,3 +317,5 @@ def _finish_run(
         ema.mark_fused(params)
     for param, copy in run.writeback:
         param.copy_(copy)
+    if ema is not None:
+        ema.stage_written(params)

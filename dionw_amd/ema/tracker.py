@@ -11,7 +11,9 @@ step updates every parameter's shadow after the optimizer's own update:
 - CPU shadows: each parameter is copied into its pinned host buffer on a copy
   stream, the training stream then waits for those copies on the GPU (no host
   wait), and ``HostEmaWorker`` applies the batch on a background thread. The
-  next due step waits for that batch before reusing the buffers.
+  next due step waits for that batch before reusing the buffers. The optimizer
+  starts the copies of the parameters each of its passes writes right after
+  that pass (``stage_written``), so they overlap the rest of the step.
 
 The reference's tracker (ema/tracker.py:40-299) blocks the host on the
 previous copy at every step instead; the cadence and the arithmetic (lerp with
@@ -106,6 +108,7 @@ class OptimizerIntegratedEMA:
         self._batch: list[HostSnapshot] = []
         self._copy_streams: dict[torch.device, torch.cuda.Stream] = {}
         self._fused: set[int] = set()
+        self._staged: set[int] = set()
 
     # -- schedule --------------------------------------------------------------
     @property
@@ -127,6 +130,7 @@ class OptimizerIntegratedEMA:
     def begin_step(self) -> None:
         """Advance the schedule as an optimizer step starts."""
         self._fused.clear()
+        self._staged.clear()
         self._count += 1
         self._now = cadence_at(self.config, self._count)
         if self._now.update and not self._on_gpu:
@@ -166,6 +170,24 @@ class OptimizerIntegratedEMA:
     def mark_fused(self, params: list[Tensor]) -> None:
         """Record that the optimizer's pass updated these parameters' shadows."""
         self._fused.update(id(p) for p in params)
+
+    @torch.no_grad()
+    def stage_written(self, params: list[Tensor]) -> None:
+        """Start the host copies of parameters the optimizer has just written
+        (CPU EMA, due step): issued after the pass that wrote them, the copies
+        overlap the rest of the step instead of following it."""
+        if self._on_gpu or not self._now.update:
+            return
+        fresh = []
+        for param in params:
+            entry = self.optimizer.state.get(param)
+            if entry is None or id(param) in self._staged:
+                continue
+            if EMA_SHADOW not in entry:
+                self._place(param, entry, None, False)
+            fresh.append((param, entry))
+            self._staged.add(id(param))
+        self._stage(fresh)
 
     # -- shadows -----------------------------------------------------------------
     def _place(self, param: Tensor, entry: dict[str, Any], shadow: Tensor | None,
@@ -210,7 +232,8 @@ class OptimizerIntegratedEMA:
             if EMA_SHADOW not in entry:
                 self._place(param, entry, None, False)
             if not self._on_gpu:
-                self._stage(param, entry)
+                if id(param) not in self._staged:
+                    self._stage([(param, entry)])
                 return
             restart = self._now.from_live or not entry[EMA_INITIALIZED]
             queue = self._copies if restart else self._lerps
@@ -219,25 +242,32 @@ class OptimizerIntegratedEMA:
             entry[EMA_INITIALIZED] = True
             entry[EMA_PENDING] = False
 
-    def _stage(self, param: Tensor, entry: dict[str, Any]) -> None:
-        if self._now.from_live:
-            entry[EMA_INITIALIZED] = False
-        staged = entry[EMA_TMP_CPU]
-        ready = None
-        if param.is_cuda and staged.is_pinned():
-            stream = self._copy_streams.get(param.device)
-            if stream is None:
-                stream = self._copy_streams[param.device] = torch.cuda.Stream(param.device)
-            stream.wait_stream(torch.cuda.current_stream(param.device))
-            with torch.cuda.stream(stream):
-                staged.copy_(param, non_blocking=True)
-                ready = torch.cuda.Event()
-                ready.record(stream)
-        else:
-            staged.copy_(param)
-        entry[EMA_EVENT] = ready
-        entry[EMA_PENDING] = True
-        self._batch.append(HostSnapshot(entry, ready, entry[EMA_SHADOW], staged))
+    def _stage(self, items: list[tuple[Tensor, dict[str, Any]]]) -> None:
+        """Copy parameters into their pinned host buffers on the copy stream,
+        which first waits for the work issued so far (the writes of the
+        parameters); one event per copy tells the worker when it has landed."""
+        joined: set[torch.device] = set()
+        for param, entry in items:
+            if self._now.from_live:
+                entry[EMA_INITIALIZED] = False
+            staged = entry[EMA_TMP_CPU]
+            ready = None
+            if param.is_cuda and staged.is_pinned():
+                stream = self._copy_streams.get(param.device)
+                if stream is None:
+                    stream = self._copy_streams[param.device] = torch.cuda.Stream(param.device)
+                if param.device not in joined:
+                    stream.wait_stream(torch.cuda.current_stream(param.device))
+                    joined.add(param.device)
+                with torch.cuda.stream(stream):
+                    staged.copy_(param, non_blocking=True)
+                    ready = torch.cuda.Event()
+                    ready.record(stream)
+            else:
+                staged.copy_(param)
+            entry[EMA_EVENT] = ready
+            entry[EMA_PENDING] = True
+            self._batch.append(HostSnapshot(entry, ready, entry[EMA_SHADOW], staged))
 
     @torch.no_grad()
     def _run_device_queues(self) -> None:
@@ -259,6 +289,7 @@ class OptimizerIntegratedEMA:
                 self._fused.clear()
                 return
             batch, self._batch = self._batch, []
+            self._staged.clear()
             if not batch:
                 return
             # Later writes of the parameters wait for the copies on the GPU.

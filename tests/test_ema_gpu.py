@@ -296,3 +296,39 @@ def test_fused_ema_equals_the_separate_pass(weight_decay: float, every: int,
     for a, b in zip(fused_w, plain_w):
         assert torch.equal(a.detach(), b.detach())
         assert torch.equal(_shadow(fused_opt, a), _shadow(plain_opt, b))
+
+
+@pytest.mark.parametrize("every", [1, 2])
+def test_cpu_ema_copies_started_after_each_pass_equal_end_of_step_copies(
+        every: int, monkeypatch: pytest.MonkeyPatch) -> None:
+    """CPU EMA: the host copies of each run's (and the AdamW group's) new
+    weights start right after the pass that wrote them; the shadows equal those
+    of copies staged after the whole step, bit for bit."""
+    from dionw_amd.ema.tracker import OptimizerIntegratedEMA
+
+    def run(early: bool):
+        with monkeypatch.context() as m:
+            if not early:
+                m.setattr(OptimizerIntegratedEMA, "stage_written", lambda self, params: None)
+            g = torch.Generator().manual_seed(5)
+            weights = [nn.Parameter(torch.randn(64, 96, generator=g).cuda()),
+                       nn.Parameter(torch.randn(64, 96, generator=g).cuda()),
+                       nn.Parameter(torch.randn(96, generator=g).cuda())]
+            opt = dionw.Dion(
+                [{"params": weights[:2], dionw.ROUTE_KEY: "matrix", dionw.FRACTION_KEY: 0.5},
+                 {"params": weights[2:], dionw.ROUTE_KEY: "adamw"}],
+                lr=1e-2, weight_decay=0.1, ema=_config(EMADevice.CPU, 0.9, every=every))
+            for _ in range(5):
+                for w in weights:
+                    w.grad = torch.randn(w.shape, generator=g).cuda()
+                opt.step()
+            opt.ema.flush_pending_updates()
+            return [_shadow(opt, w).clone() for w in weights], [w.detach().cpu() for w in weights]
+
+    early_shadows, early_weights = run(True)
+    late_shadows, late_weights = run(False)
+    for a, b in zip(early_weights, late_weights):
+        assert torch.equal(a, b)
+    for a, b in zip(early_shadows, late_shadows):
+        assert a.device.type == "cpu" and torch.equal(a, b)
+    assert not torch.equal(early_shadows[0], early_weights[0])  # a real lerp, not a copy
