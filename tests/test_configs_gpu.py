@@ -66,7 +66,7 @@ def _student_t(g: torch.Generator, *shape: int) -> torch.Tensor:
 
 def _check_run(name: str, params: list[nn.Parameter], opt: Dion, before: torch.Tensor,
                w_ref: torch.Tensor, mom_ref: torch.Tensor, var_ref: torch.Tensor,
-               update_bar: float, blocks_per_param: int = 1) -> None:
+               update_bar: float) -> None:
     """GPU state of ``params`` (stacked into [blocks, rows, cols]) against the
     oracle's after the same step from the same state ``before``."""
     shape = w_ref.shape
@@ -79,7 +79,6 @@ def _check_run(name: str, params: list[nn.Parameter], opt: Dion, before: torch.T
     assert rel_fro(got_w, w_ref) < 2e-3, f"{name}: parameters"
     got_v = torch.stack([opt.state[p]["variance"].cpu() for p in params]).view(var_ref.shape)
     assert rel_fro(got_v, var_ref) < 2e-2, f"{name}: NorMuon variance"
-    del blocks_per_param
 
 
 # ---- products at the tile counts that switch on XCD run dealing ---------------
@@ -333,8 +332,8 @@ def test_config5a_moe_dion_with_gpu_ema() -> None:
 
 
 def test_config5b_moe_muon_update() -> None:
-    """The same 64 experts with MUON_UPDATE (Keller bfloat16 quintic, Nesterov,
-    every row, no row normalization). Two steps; momentum bit for bit on every
+    """The same 64 experts with MUON_UPDATE (KELLER_TRITON bfloat16 quintic,
+    Nesterov, every row, no row normalization). Two steps; momentum bit for bit on every
     expert, experts 0 and 63 (six blocks) against the oracle."""
     _say("config 5b: MoE MUON_UPDATE, 2 steps")
     g = torch.Generator(device=DEV).manual_seed(0)
@@ -358,8 +357,8 @@ def test_config5b_moe_muon_update() -> None:
             w = before[i].clone()
             var = torch.zeros(1, w.shape[1], 1)
             dion_ref.step_blocks(w, experts[i].grad.cpu()[None], ref_m[i], var, k=w.shape[1],
-                                 lr=LR, mu=MU, beta2=BETA2, weight_decay=WD, kind="keller",
-                                 normuon=False, nesterov=True)
+                                 lr=LR, mu=MU, beta2=BETA2, weight_decay=WD,
+                                 kind="keller_triton", normuon=False, nesterov=True)
             got = experts[i].detach().cpu()[None]
             err = rel_fro(got - before[i] * decay, w - before[i] * decay)
             assert err < 3e-2, f"step {step} expert block {i}: update rel err {err}"
