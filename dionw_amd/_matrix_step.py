@@ -49,6 +49,7 @@ from dionw_amd.newton_schulz import (
     NewtonSchulzCall,
     group_launches,
     newton_schulz_call,
+    padded_sides,
     prepared_inputs,
     prepared_orientations,
     run_newton_schulz,
@@ -119,10 +120,6 @@ def _step_size(bucket: Bucket, lr: float) -> float:
     )
 
 
-def _round8(n: int) -> int:
-    return (n + 7) // 8 * 8
-
-
 # Dion.step sets this around its bucket loop: step_run then queues each fused
 # run after its momentum passes, and the queue finishes the queued runs
 # together, with one grouped Newton-Schulz call (small runs fill the CUs that
@@ -180,7 +177,7 @@ class RunQueue:
 
 def _ns_bytes(ortho: HipOrthogonalize, blocks: int, k: int, cols: int) -> int:
     """Bytes of a fused run's Newton-Schulz buffers (inputs, output, workspace)."""
-    p_pad, j_pad = _round8(k), _round8(cols)
+    p_pad, j_pad = padded_sides(k, cols)
     r, c = min(p_pad, j_pad), max(p_pad, j_pad)
     work = int(_lib.library().dionw_newton_schulz_workspace(ortho.lib_kind, blocks, r, c))
     inputs = sum(prepared_orientations(k, cols))
@@ -245,7 +242,7 @@ def step_run(
         # Only the orientations the iteration reads are written.
         xr, xt = prepared_inputs(ortho, device, blocks, k, cols, "ns_xr" + own, "ns_xt" + own)
         _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
-                  den.data_ptr(), blocks, rows, cols, k, _round8(k), _round8(cols), mu,
+                  den.data_ptr(), blocks, rows, cols, k, *padded_sides(k, cols), mu,
                   int(nesterov), 1, ortho.elem, None if xr is None else xr.data_ptr(),
                   None if xt is None else xt.data_ptr(), stream)
         orthogonal = _workspace.buffer(device, "ns_out" + own, (blocks, k, cols), torch.bfloat16)

@@ -59,6 +59,27 @@ def _round8(n: int) -> int:
     return (n + 7) // 8 * 8
 
 
+# Whether an iterate whose short side is an odd multiple of 32 (at least 256)
+# is padded with zero rows to the next multiple of 64.
+PAD_SHORT_SIDE_TO_64 = True
+
+
+def padded_sides(rows: int, cols: int) -> tuple[int, int]:
+    """The padded extents ``(p_pad, j_pad)`` of a ``[rows, cols]`` block's
+    prepared input: both sides rounded up to 8; a short side that is then an odd
+    multiple of 32 (at least 256) grows by 32 more, so that the products whose
+    depth is that side run 64-deep LDS stages (the padding rows are zero, which
+    every polynomial here keeps exactly zero, and are never stored)."""
+    p_pad, j_pad = _round8(rows), _round8(cols)
+    short = min(p_pad, j_pad)
+    if PAD_SHORT_SIDE_TO_64 and short >= 256 and short % 64 == 32:
+        if rows <= cols:
+            p_pad += 32
+        else:
+            j_pad += 32
+    return p_pad, j_pad
+
+
 def prepared_orientations(rows: int, cols: int) -> tuple[bool, bool]:
     """Which prepared inputs the iteration on ``[rows, cols]`` blocks reads:
     (weight orientation, its transpose).
@@ -69,7 +90,7 @@ def prepared_orientations(rows: int, cols: int) -> tuple[bool, bool]:
     itself as a ``[k, n]`` operand (``dionw_newton_schulz``).
     """
     tall = rows > cols
-    other = _round8(min(rows, cols)) % 32 != 0
+    other = min(padded_sides(rows, cols)) % 32 != 0
     return (other, True) if tall else (True, other)
 
 
@@ -80,7 +101,7 @@ def prepared_inputs(
     """Scratch buffers for the prepared inputs of ``[blocks, rows, cols]``: the
     weight orientation ``[blocks, round8(rows), round8(cols)]`` and its
     transpose, each None when the iteration does not read it."""
-    p_pad, j_pad = _round8(rows), _round8(cols)
+    p_pad, j_pad = padded_sides(rows, cols)
     want_xr, want_xt = prepared_orientations(rows, cols)
     xr = (_workspace.buffer(device, name_xr, (blocks, p_pad, j_pad), ortho.dtype)
           if want_xr else None)
@@ -142,7 +163,7 @@ class HipOrthogonalize:
         xr, xt = prepared_inputs(self, device, blocks, rows, cols, "ortho_xr", "ortho_xt")
         _lib.call("dionw_normalize_input", source.data_ptr(), _INPUT_ELEMS[source.dtype], blocks,
                   rows, cols, self.norm_safety, float(epsilon), rowsq.data_ptr(), den.data_ptr(),
-                  _round8(rows), _round8(cols), self.elem, _ptr(xr), _ptr(xt), stream)
+                  *padded_sides(rows, cols), self.elem, _ptr(xr), _ptr(xt), stream)
         run_newton_schulz(self, blocks, rows, cols, xr, xt, out, stream)
         return out if matrix.ndim == 3 else out[0]
 
@@ -191,10 +212,11 @@ def newton_schulz_call(
         ValueError: If an input the iteration reads is None.
     """
     tall = rows > cols
+    p_pad, j_pad = padded_sides(rows, cols)
     if tall:
-        x, x_t, r, c, r_real, c_real = xt, xr, _round8(cols), _round8(rows), cols, rows
+        x, x_t, r, c, r_real, c_real = xt, xr, j_pad, p_pad, cols, rows
     else:
-        x, x_t, r, c, r_real, c_real = xr, xt, _round8(rows), _round8(cols), rows, cols
+        x, x_t, r, c, r_real, c_real = xr, xt, p_pad, j_pad, rows, cols
     if x is None or (x_t is None and r % 32 != 0):
         raise ValueError(f"newton_schulz_call: [{rows}, {cols}] blocks need the prepared "
                          f"inputs {prepared_orientations(rows, cols)} (weight orientation, "
