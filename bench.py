@@ -542,6 +542,11 @@ def main() -> int:
         },
         "gram_ns_tflops": round(ns_tflops, 1),
         "momentum_pass_gbs": round(acc_gbs, 1),
+        # The momentum pass (M += G with the row scores; 12 B per element) against
+        # the HBM roofline.
+        "momentum_roofline": {"bound": "hbm", "achieved": round(acc_gbs, 1),
+                              "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                              "frac": round(acc_gbs / PEAK_HBM_GBS, 4)} if acc_gbs else None,
         "host_dispatch_ms": round(host_dispatch, 3),
         "phases": phases,
         "roofline": {
