@@ -249,6 +249,172 @@ def gram_ns_bench(torch, steps: int, warmup: int) -> dict:
     }
 
 
+# The reference's README performance table (bench/optimizer_step.py:40-196):
+# a pre-norm transformer of width 2048, depth 24, 16 heads and a 32000-token
+# vocabulary (1.34 G parameters), random gradients 1e-3 N(0,1), lr 1e-4,
+# betas (0.9, 0.95), no weight decay; only ``step()`` is timed, as the median
+# of 20 single-step timings after 5 warm-up steps.
+TRANSFORMER = {"width": 2048, "depth": 24, "heads": 16, "vocab": 32000}
+TABLE_WARMUP, TABLE_TIMED = 5, 20
+# Published step times of the default rule at f=0.25 (README.md:491-507).
+TRANSFORMER_PUBLISHED_MS = {"RTX 4090": 92.5, "RTX 5090": 61.0, "GH200": 27.2}
+# The wide blocks of the reference's Newton-Schulz table (bench/newton_schulz.py:19-24).
+WIDE_SHAPES = ((28, 576, 1152), (28, 576, 4608), (28, 1152, 4608), (16, 1024, 8192))
+
+
+def median_step_ms(torch, call, warmup: int = TABLE_WARMUP, timed: int = TABLE_TIMED) -> float:
+    """Median GPU time of ``call`` over ``timed`` calls timed one by one with
+    events on the current stream, after ``warmup`` untimed calls."""
+    import statistics
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(timed):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        call()
+        end.record()
+        end.synchronize()
+        samples.append(start.elapsed_time(end))
+    return statistics.median(samples)
+
+
+def build_transformer(torch, dev):
+    """The README table's transformer on ``dev`` with a gradient on every
+    parameter; each block declares its fused QKV projection as 3 * heads
+    separate matrices."""
+    import dionw_amd
+
+    nn = torch.nn
+    spec = TRANSFORMER
+
+    class Block(nn.Module):
+        def __init__(self, width: int, heads: int) -> None:
+            super().__init__()
+            self.heads = heads
+            self.norm1, self.norm2 = nn.LayerNorm(width), nn.LayerNorm(width)
+            self.qkv = nn.Linear(width, 3 * width)
+            self.proj = nn.Linear(width, width)
+            self.fc1 = nn.Linear(width, 4 * width)
+            self.fc2 = nn.Linear(4 * width, width)
+
+        def dion_routes(self):
+            return ((self.qkv.weight,
+                     dionw_amd.Route(dionw_amd.RouteKind.MATRIX, num_heads=3 * self.heads)),)
+
+    class Transformer(nn.Module):
+        def __init__(self) -> None:
+            super().__init__()
+            self.embed = nn.Embedding(spec["vocab"], spec["width"])
+            self.blocks = nn.ModuleList(Block(spec["width"], spec["heads"])
+                                        for _ in range(spec["depth"]))
+            self.norm = nn.LayerNorm(spec["width"])
+            self.head = nn.Linear(spec["width"], spec["vocab"], bias=False)
+
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Transformer()
+    for param in model.parameters():
+        param.grad = torch.randn_like(param) * 1e-3
+    return model
+
+
+def transformer_table(torch) -> dict:
+    """Step time of each optimizer of the README table on one MI355X, and the
+    host dispatch time of the default step."""
+    import gc
+
+    import dionw_amd
+
+    dev = torch.device("cuda:0")
+
+    def dion(model, fraction, selection_min_dim, kind):
+        groups, _ = dionw_amd.param_groups(model, fraction=fraction,
+                                           selection_min_dim=selection_min_dim, min_matrix_dim=8)
+        return dionw_amd.Dion(groups, lr=1e-4, betas=(0.9, 0.95), weight_decay=0.0,
+                              matrix_update=dionw_amd.MatrixUpdate(
+                                  newton_schulz=kind,
+                                  row_normalization=dionw_amd.RowNormalization.NORMUON,
+                                  momentum_form=dionw_amd.MomentumForm.HEAVY_BALL))
+
+    ns = dionw_amd.NewtonSchulz
+    variants = {
+        "dionw, f=0.25, default rule": lambda m: dion(m, 0.25, 1024, ns.GRAM),
+        "dionw, f=0.25, every block, Gram": lambda m: dion(m, 0.25, 1, ns.GRAM),
+        "dionw, f=0.25, every block, Polar Express Triton":
+            lambda m: dion(m, 0.25, 1, ns.POLAR_EXPRESS_TRITON),
+        "dionw, f=0.5, default rule": lambda m: dion(m, 0.5, 1024, ns.GRAM),
+        "fused AdamW (torch), all parameters":
+            lambda m: torch.optim.AdamW(m.parameters(), lr=1e-4, betas=(0.9, 0.95), fused=True),
+    }
+    table, host, n_params = {}, None, 0
+    for name, make in variants.items():
+        print(f"[bench] transformer-1.34b: {name}", file=sys.stderr, flush=True)
+        model = build_transformer(torch, dev)
+        n_params = sum(p.numel() for p in model.parameters())
+        opt = make(model)
+        table[name] = round(median_step_ms(torch, opt.step), 3)
+        if host is None:
+            host = host_dispatch_ms(torch, opt, samples=TABLE_TIMED)
+        del opt, model
+        gc.collect()
+        torch.cuda.empty_cache()
+    value = table["dionw, f=0.25, default rule"]
+    return {
+        "metric": "Dion step ms, 1.34B transformer, f=0.25 default rule (README table)",
+        "value": value, "unit": "ms", "n_gpus": 1, "steps": TABLE_TIMED, "warmup": TABLE_WARMUP,
+        "ms_per_step": value, "higher_is_better": False, "scaling": "weak",
+        # Against the GH200 figure of README.md:507 (lower is better).
+        "vs_baseline": round(value / TRANSFORMER_PUBLISHED_MS["GH200"], 4),
+        "dtype": "f32 state, f16 MFMA Newton-Schulz", "data": "synthetic",
+        "config": {"workload": "transformer-1.34b: width 2048, depth 24, 16 heads, vocab 32000, "
+                               "QKV split per head, default routing; median of 20 steps",
+                   "params": n_params},
+        "variants_ms": table,
+        "host_dispatch_ms": round(host, 3),
+        "published_ms": TRANSFORMER_PUBLISHED_MS,
+    }
+
+
+def wide_ns_table(torch) -> dict:
+    """Gram Newton-Schulz against both Polar Express variants on the reference's
+    wide blocks: median ms of one batched call on a float32 N(0,1) batch."""
+    from dionw_amd.newton_schulz import NewtonSchulz, newton_schulz_fn
+
+    dev = torch.device("cuda:0")
+    kinds = (NewtonSchulz.GRAM, NewtonSchulz.POLAR_EXPRESS_TRITON, NewtonSchulz.POLAR_EXPRESS)
+    rows = []
+    for shape in WIDE_SHAPES:
+        torch.manual_seed(0)
+        x = torch.randn(*shape, device=dev)
+        ms = {kind.value: median_step_ms(torch, lambda k=kind: newton_schulz_fn(k)(x, 1e-7))
+              for kind in kinds}
+        blocks, r, c = shape
+        gram = ms[NewtonSchulz.GRAM.value]
+        rows.append({
+            "shape": "x".join(map(str, shape)),
+            "ms": {k: round(v, 4) for k, v in ms.items()},
+            "gram_tflops": round(blocks * ns_flops(0, r, c) / (gram * 1e-3) / 1e12, 1),
+            "speedup_vs_triton": round(ms[NewtonSchulz.POLAR_EXPRESS_TRITON.value] / gram, 3),
+            "speedup_vs_cublas": round(ms[NewtonSchulz.POLAR_EXPRESS.value] / gram, 3),
+        })
+        print(f"[bench] ns-wide {rows[-1]}", file=sys.stderr, flush=True)
+    worst = min(row["speedup_vs_triton"] for row in rows)
+    return {
+        "metric": "Gram NS speedup over Polar Express (Triton products), wide blocks, minimum",
+        "value": worst, "unit": "x", "n_gpus": 1, "steps": TABLE_TIMED, "warmup": TABLE_WARMUP,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 MFMA (Gram), bf16 MFMA (Polar Express)", "data": "synthetic",
+        "config": {"workload": "ns-wide: " + ", ".join(r["shape"] for r in rows)},
+        "rows": rows,
+        # README.md:536-539: RTX 4090 / RTX 5090 / GH200.
+        "published_speedup_vs_triton": ["1.2-1.9", "1.3-2.7", "1.05-1.8"],
+        "published_speedup_vs_cublas": ["1.5-2.5", "1.9-3.5", "1.1-2.2"],
+    }
+
+
 def cpu_share() -> dict:
     """The host CPUs this process may use: the affinity set, capped by a cgroup
     CPU quota (a GPU box grants each job a share of a larger host), with the
@@ -433,7 +599,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=5)
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--config", default="llama3-8b",
-                        choices=["llama3-8b", "gpt2-small", "gram-ns", "moe", "moe-muon"])
+                        choices=["llama3-8b", "gpt2-small", "gram-ns", "moe", "moe-muon",
+                                 "transformer-1.34b", "ns-wide"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--instrumented-steps", type=int, default=2)
     args = parser.parse_args()
@@ -451,6 +618,12 @@ def main() -> int:
 
     if args.config == "gram-ns":
         print(json.dumps(gram_ns_bench(torch, args.steps, args.warmup)), flush=True)
+        return 0
+    if args.config == "transformer-1.34b":
+        print(json.dumps(transformer_table(torch)), flush=True)
+        return 0
+    if args.config == "ns-wide":
+        print(json.dumps(wide_ns_table(torch)), flush=True)
         return 0
     dev = torch.device("cuda:0")
     spec = LLAMA if args.config == "llama3-8b" else GPT2

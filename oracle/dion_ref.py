@@ -127,22 +127,24 @@ def _baddbmm(c: Tensor, a: Tensor, b: Tensor, beta: float) -> Tensor:
     return (_mm(a, b) + beta * c.float()).to(c.dtype)
 
 
-def _gram(x: Tensor) -> Tensor:
-    """_gram.py:50-69 on wide float16 ``x`` [N, r, c]."""
+def _gram(x: Tensor, restart: int | None = GRAM_RESTART_ITERATION) -> Tensor:
+    """_gram.py:50-69 on wide float16 ``x`` [N, r, c]. ``restart=None`` never
+    re-forms the Gram matrix from the iterate (a variant for tests that show
+    what the restart buys)."""
     gram = ns_line_1(x)
     eye = torch.eye(x.size(-2), dtype=torch.float32).expand(gram.shape)
     q = None
     last = len(GRAM_COEFFICIENTS) - 1
     for i, (a, b, c) in enumerate(GRAM_COEFFICIENTS):
-        if i == GRAM_RESTART_ITERATION:
+        if i == restart:
             x = _mm(q, x).to(x.dtype)
             gram = ns_line_1(x)
         z = ns_line_2(gram, c, b)
-        if i in (0, GRAM_RESTART_ITERATION):
+        if i in (0, restart):
             q = (z.float() + a * eye).to(x.dtype)
         else:
             q = _baddbmm(q, q, z, a)
-        if i < last and i + 1 != GRAM_RESTART_ITERATION:
+        if i < last and i + 1 != restart:
             rz = _baddbmm(gram, gram, z, a)
             gram = _baddbmm(rz, z, rz, a)
     return _mm(q, x).to(x.dtype)
@@ -156,14 +158,15 @@ def _standard(x: Tensor) -> Tensor:
     return x
 
 
-def gram_polar_express(matrix: Tensor, epsilon: float) -> Tensor:
+def gram_polar_express(matrix: Tensor, epsilon: float,
+                       restart: int | None = GRAM_RESTART_ITERATION) -> Tensor:
     """_gram.py:72-89: Gram Newton-Schulz of a [N, rows, cols] batch, bf16 out."""
     tall = matrix.size(-2) > matrix.size(-1)
     x = matrix.mT if tall else matrix
     x = x.float()
     norm = torch.linalg.vector_norm(x, dim=(-2, -1), keepdim=True)
     x = (x / (norm + epsilon)).half().contiguous()
-    x = _gram(x) if x.size(-1) > x.size(-2) else _standard(x)
+    x = _gram(x, restart) if x.size(-1) > x.size(-2) else _standard(x)
     return (x.mT if tall else x).bfloat16()
 
 

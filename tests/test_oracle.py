@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from oracle import dion_ref
+from tests import spectra
 from tests.conftest import rel_fro
 
 COEFFICIENTS = json.loads(
@@ -122,6 +123,37 @@ def test_gram_vs_float64_polynomial(shape) -> None:
     target = dion_ref.polynomial_float64(x, dion_ref.GRAM_COEFFICIENTS, 1.0)
     err = rel_fro(dion_ref.gram_polar_express(x, 1e-7).float(), target)
     assert err < 0.006, err
+
+
+@pytest.mark.parametrize("spectrum", spectra.SPECTRA[1:])
+def test_spectrum_matrices_have_their_singular_values(spectrum) -> None:
+    """The test matrices carry the singular values they are named for."""
+    x = spectra.spectrum_matrix(spectrum)
+    assert x.shape == (1, *spectra.SHAPE) and x.dtype == torch.float32
+    got = torch.linalg.svdvals(x[0].double())
+    want = spectra.singular_values(spectrum, spectra.SHAPE[0])
+    assert torch.allclose(got, want, rtol=1e-3, atol=1e-6)
+
+
+@pytest.mark.parametrize("spectrum", spectra.ILL_CONDITIONED)
+def test_gram_restart_bounds_rounding_on_ill_conditioned_spectra(spectrum) -> None:
+    """test_newton_schulz.py:79-92 and :137-148 on the oracle: with singular
+    values spread over decades, Gram in float16 stays within 0.08 of its
+    float64 polynomials because of the restart (without it the iterated Gram
+    matrix compounds its rounding past 0.1), rounds less than Polar Express in
+    bfloat16, and a bfloat16 input costs it more than 1.8x."""
+    x = spectra.spectrum_matrix(spectrum)
+    gram_target = dion_ref.polynomial_float64(x, dion_ref.GRAM_COEFFICIENTS, 1.0)
+    pe_target = dion_ref.polynomial_float64(
+        x, dion_ref.POLAR_EXPRESS_COEFFICIENTS, dion_ref.POLAR_EXPRESS_NORM_SAFETY)
+    gram = rel_fro(dion_ref.gram_polar_express(x, 1e-7).float(), gram_target)
+    no_restart = rel_fro(dion_ref.gram_polar_express(x, 1e-7, restart=None).float(), gram_target)
+    bf16_input = rel_fro(dion_ref.gram_polar_express(x.bfloat16(), 1e-7).float(), gram_target)
+    polar_express = rel_fro(dion_ref.polar_express(x, 1e-7).float(), pe_target)
+    assert gram < 0.08, gram
+    assert no_restart > 0.1, no_restart
+    assert gram < polar_express, (gram, polar_express)
+    assert bf16_input > 1.8 * gram, (bf16_input, gram)
 
 
 @pytest.mark.parametrize("shape", [(3, 64, 256), (3, 256, 64), (3, 128, 128), (96, 160)])
