@@ -17,6 +17,7 @@ Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--no-cpu-baseli
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -91,10 +92,14 @@ class Timeline:
             entry["calls"] += 1
             a = meta["args"]
             if name == "dionw_newton_schulz":
-                kind, batch, r_real, c_real = a[0], a[1], a[6], a[7]
+                kind, batch, r, c, r_real, c_real = a[0], a[1], a[2], a[3], a[6], a[7]
                 entry["flops"] += batch * ns_flops(kind, r_real, c_real)
-                # MFMA product launches of the call: 18 for the Gram iteration, 15 otherwise.
-                entry["launches"] = entry.get("launches", 0) + (18 if kind == 0 and c_real > r_real else 15)
+                # The library's own count of the product launches of the call.
+                one = lambda t, v: (t * 1)(v)
+                entry["launches"] = entry.get("launches", 0) + self._restore[0].library(
+                ).dionw_newton_schulz_group_launches(
+                    1, one(ctypes.c_int32, kind), one(ctypes.c_int64, batch), one(ctypes.c_int64, r),
+                    one(ctypes.c_int64, c), one(ctypes.c_int64, r_real), one(ctypes.c_int64, c_real))
             elif name == "dionw_newton_schulz_group":
                 # Reported with the single calls: the same products, grouped.
                 del out[name]

@@ -67,6 +67,7 @@ struct Problem {
   int out_mode;
   int64_t batch;
   GemmArgs g;
+  int with_next;  // independent of the program's next product: they may share a launch
 };
 
 template <typename T>
@@ -981,13 +982,12 @@ int launch_pipe(const Problem& p, hipStream_t stream) {
   return launch_pipe_kn<T, OUT_T, MODE, CFG, false>(p, stream);
 }
 
-// One launch of up to kMaxGroup products on 256x256 tiles with 64-deep stages,
-// longest k first (its tiles take longest, so they start first).
-template <typename T, typename OUT_T, int MODE, bool BKN>
+// One launch of up to kMaxGroup products on one tile configuration with
+// 64-deep stages, longest k first (its tiles take longest, so they start first).
+template <typename T, typename OUT_T, int MODE, typename CFG, bool BKN>
 int launch_pipe_group_kn(const std::vector<const Problem*>& ps, hipStream_t stream) {
-  using Big64 = PipeCfg<256, 256, 4, 4, 2, 64>;
-  constexpr size_t lds_bytes = pipe_lds_bytes<Big64>();
-  constexpr auto kern = gemm_nt_pipe_group_kernel<T, OUT_T, MODE, Big64, BKN>;
+  constexpr size_t lds_bytes = pipe_lds_bytes<CFG>();
+  constexpr auto kern = gemm_nt_pipe_group_kernel<T, OUT_T, MODE, CFG, BKN>;
   DIONW_TRY(allow_lds<kern>(lds_bytes));
   std::vector<const Problem*> order(ps);
   std::stable_sort(order.begin(), order.end(),
@@ -996,7 +996,7 @@ int launch_pipe_group_kn(const std::vector<const Problem*>& ps, hipStream_t stre
   grp.count = (int)order.size();
   int64_t start = 0;
   for (int q = 0; q < grp.count; ++q) {
-    const int64_t wgs = pipe_args<Big64>(*order[q], grp.g[q]);
+    const int64_t wgs = pipe_args<CFG>(*order[q], grp.g[q]);
     if (wgs < 0) return kInvalid;
     grp.batch[q] = (int)order[q]->batch;
     grp.start[q] = (int)start;
@@ -1006,14 +1006,24 @@ int launch_pipe_group_kn(const std::vector<const Problem*>& ps, hipStream_t stre
       return kInvalid;
     }
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)start), dim3(Big64::threads), lds_bytes, stream, grp);
+  hipLaunchKernelGGL(kern, dim3((unsigned)start), dim3(CFG::threads), lds_bytes, stream, grp);
   return check_launch("gemm_nt_pipe_group");
 }
 
+// Tile of a grouped launch: 256x256 (16 waves, one workgroup per CU) or
+// 128x128 (4 waves, two per CU).
+enum GroupTile : int { kNoGroup = 0, kGroupBig = 1, kGroupMid = 2 };
+
 template <typename T, typename OUT_T, int MODE>
-int launch_pipe_group(const std::vector<const Problem*>& ps, hipStream_t stream) {
-  if (ps[0]->g.b_kn) return launch_pipe_group_kn<T, OUT_T, MODE, true>(ps, stream);
-  return launch_pipe_group_kn<T, OUT_T, MODE, false>(ps, stream);
+int launch_pipe_group(const std::vector<const Problem*>& ps, GroupTile tile, hipStream_t stream) {
+  using Big64 = PipeCfg<256, 256, 4, 4, 2, 64>;
+  using Mid64 = PipeCfg<128, 128, 2, 2, 2, 64>;
+  const bool kn = ps[0]->g.b_kn;
+  if (tile == kGroupMid)
+    return kn ? launch_pipe_group_kn<T, OUT_T, MODE, Mid64, true>(ps, stream)
+              : launch_pipe_group_kn<T, OUT_T, MODE, Mid64, false>(ps, stream);
+  return kn ? launch_pipe_group_kn<T, OUT_T, MODE, Big64, true>(ps, stream)
+            : launch_pipe_group_kn<T, OUT_T, MODE, Big64, false>(ps, stream);
 }
 
 // Workgroups a tile size yields (symmetric products: upper-triangle tiles).
@@ -1108,27 +1118,44 @@ int launch(const Problem& p, hipStream_t stream) {
   return kInvalid;
 }
 
-// Whether one grouped launch beats one launch per product. Time in 256x256
-// rounds times k: each product alone takes its better tile (the launcher's
-// rule); grouped, the 256x256 tiles of all of them fill the CUs longest first,
-// which costs their total work over the 256 CUs plus about half a round of the
-// shortest tiles, and no less than the longest tile.
-bool group_pays(const std::vector<const Problem*>& ps) {
-  double separate = 0.0, work = 0.0, kmax = 0.0, kmin = 1e300;
+// Whether one grouped launch beats one launch per product, and on which tile.
+// Time in 256x256 rounds times k (a round of 256x256 tiles over depth k costs
+// k, a round of two 128x128 tiles per CU 0.6 k). Alone, each product takes its
+// better tile (the launcher's rule); grouped, the tiles of all of them fill the
+// CUs longest first, which costs their total work over the CUs plus about half
+// a round of the shortest tiles, and no less than the longest tile.
+//
+// The same product of several runs (walk_groups' positions) groups on 256x256
+// tiles on that estimate alone. Two independent products of one run, each one
+// round of workgroups or less, also count the ramp and drain of a launch
+// (kRamp, about 11 us: a third of a 256x256 round at k = 1024) and may group on
+// either tile: two launches of one round each cost two ramps; one launch of
+// both, one ramp and the rounds their tiles fill together. (Counting the ramp
+// for the runs' positions too measured slower on GPT-2-small's runs, whose
+// products then group on 128x128 tiles.)
+constexpr double kRamp = 340.0;
+
+GroupTile group_plan(const std::vector<const Problem*>& ps, bool pair) {
+  const double ramp = pair ? kRamp : 0.0;
+  double separate = 0.0, big = 0.0, mid = 0.0, kmax = 0.0, kmin = 1e300;
   for (const Problem* p : ps) {
     const double k = (double)p->g.k;
-    separate += k * 0.1 * (double)std::min(big_tenths(*p), mid_tenths(*p));
-    work += k * (double)wgs_of(*p, 256) / 256.0;
+    separate += ramp + k * 0.1 * (double)std::min(big_tenths(*p), mid_tenths(*p));
+    big += k * (double)wgs_of(*p, 256) / 256.0;
+    mid += 0.6 * k * (double)wgs_of(*p, 128) / 512.0;
     kmax = std::max(kmax, k);
     kmin = std::min(kmin, k);
   }
-  return std::max(work + 0.5 * kmin, kmax) < separate;
+  const double big_cost = ramp + std::max(big + 0.5 * kmin, kmax);
+  const double mid_cost = pair ? ramp + std::max(mid + 0.3 * kmin, 0.6 * kmax) : 1e300;
+  if (std::min(big_cost, mid_cost) >= separate) return kNoGroup;
+  return mid_cost < big_cost ? kGroupMid : kGroupBig;
 }
 
 // Independent products in as few launches as possible: one grouped launch when
 // every product has the same types and a k depth that is a multiple of 64 (the
-// 256x256 tile with 64-deep stages serves them all) and grouping pays, else one
-// launch each.
+// tiles with 64-deep stages serve them all) and grouping pays, else one launch
+// each.
 std::vector<const Problem*> live_products(const std::vector<const Problem*>& ps) {
   std::vector<const Problem*> live;
   for (const Problem* p : ps)
@@ -1136,29 +1163,30 @@ std::vector<const Problem*> live_products(const std::vector<const Problem*>& ps)
   return live;
 }
 
-bool groups(const std::vector<const Problem*>& live) {
+GroupTile groups(const std::vector<const Problem*>& live, bool pair = false) {
   bool together = live.size() >= 2 && live.size() <= (size_t)kMaxGroup;
   for (const Problem* p : live)
     together = together && p->elem == live[0]->elem && p->out_mode == live[0]->out_mode &&
                p->g.b_kn == live[0]->g.b_kn && p->g.k % 64 == 0 && p->batch <= INT32_MAX &&
                operands_ok(p->g) && !(p->g.b_kn && (p->g.n % 8 || p->g.sym));
-  return together && group_pays(live);
+  return together ? group_plan(live, pair) : kNoGroup;
 }
 
-int launch_group(const std::vector<const Problem*>& ps, hipStream_t stream) {
+int launch_group(const std::vector<const Problem*>& ps, hipStream_t stream, bool pair = false) {
   const std::vector<const Problem*> live = live_products(ps);
-  if (!groups(live)) {
+  const GroupTile tile = groups(live, pair);
+  if (tile == kNoGroup) {
     for (const Problem* p : live) DIONW_TRY(launch(*p, stream));
     return kOk;
   }
   if (live[0]->elem == kF16) {
     if (live[0]->out_mode == kOutBf16ViaF16)
-      return launch_pipe_group<_Float16, __bf16, kOutBf16ViaF16>(live, stream);
-    return launch_pipe_group<_Float16, _Float16, kOutSame>(live, stream);
+      return launch_pipe_group<_Float16, __bf16, kOutBf16ViaF16>(live, tile, stream);
+    return launch_pipe_group<_Float16, _Float16, kOutSame>(live, tile, stream);
   }
   if (live[0]->out_mode == kOutRoundAcc)
-    return launch_pipe_group<__bf16, __bf16, kOutRoundAcc>(live, stream);
-  return launch_pipe_group<__bf16, __bf16, kOutSame>(live, stream);
+    return launch_pipe_group<__bf16, __bf16, kOutRoundAcc>(live, tile, stream);
+  return launch_pipe_group<__bf16, __bf16, kOutSame>(live, tile, stream);
 }
 
 // ---- Newton-Schulz drivers ---------------------------------------------------
@@ -1404,11 +1432,13 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
       }
       prog.push_back(p);
       if (i != 0 && i != 2) {
-        // Q = a Q + Q Z
+        // Q = a Q + Q Z (independent of the RZ product that follows it at
+        // iteration 3: both read Z, neither writes what the other reads).
         p = product(elem, batch, R, R, R, Q, Z);
         set_addend(p, Q, 1.f, a);
         set_out(p, Q2);
         make_symmetric(p);
+        p.with_next = i < 4 && i + 1 != 2;
         prog.push_back(p);
         std::swap(Q, Q2);
       }
@@ -1488,14 +1518,17 @@ int ns_program(int32_t kind, int64_t batch, int64_t r, int64_t c, void* x, void*
 bool same_structure(const std::vector<Problem>& a, const std::vector<Problem>& b) {
   if (a.size() != b.size()) return false;
   for (size_t i = 0; i < a.size(); ++i)
-    if (a[i].elem != b[i].elem || a[i].out_mode != b[i].out_mode || a[i].g.b_kn != b[i].g.b_kn)
+    if (a[i].elem != b[i].elem || a[i].out_mode != b[i].out_mode ||
+        a[i].g.b_kn != b[i].g.b_kn || a[i].with_next != b[i].with_next)
       return false;
   return true;
 }
 
-// Runs whose sequences match product by product (length and types) go
-// together, kMaxGroup at a time: one launch per position of the sequence when
-// grouping pays. Counts the launches in *launches and, if issue, launches them.
+// Runs whose sequences match product by product (length, types and
+// independence) go together, kMaxGroup at a time: one launch per position of
+// the sequence when grouping pays; a run on its own also shares one launch
+// between two independent products when that pays. Counts the launches in *launches and, if issue,
+// launches them.
 int walk_groups(const std::vector<std::vector<Problem>>& progs, bool issue, hipStream_t stream,
                 int64_t* launches) {
   const int count = (int)progs.size();
@@ -1509,11 +1542,21 @@ int walk_groups(const std::vector<std::vector<Problem>>& progs, bool issue, hipS
         runs.push_back(j);
         done[j] = 1;
       }
-    for (size_t pos = 0; pos < progs[i].size(); ++pos) {
+    const std::vector<Problem>& prog = progs[i];
+    for (size_t pos = 0; pos < prog.size(); ++pos) {
+      if (prog[pos].with_next && pos + 1 < prog.size() && runs.size() == 1) {
+        const std::vector<const Problem*> pair{&prog[pos], &prog[pos + 1]};
+        if (groups(live_products(pair), true) != kNoGroup) {
+          *launches += 1;
+          if (issue) DIONW_TRY(launch_group(pair, stream, true));
+          ++pos;
+          continue;
+        }
+      }
       std::vector<const Problem*> ps;
       for (int j : runs) ps.push_back(&progs[j][pos]);
       const std::vector<const Problem*> live = live_products(ps);
-      *launches += groups(live) ? 1 : (int64_t)live.size();
+      *launches += groups(live) != kNoGroup ? 1 : (int64_t)live.size();
       if (issue) DIONW_TRY(launch_group(ps, stream));
     }
   }
@@ -1529,11 +1572,11 @@ int dionw_newton_schulz(int32_t kind, int64_t batch, int64_t r, int64_t c, void*
                         int64_t r_real, int64_t c_real, void* out, int32_t out_transposed,
                         int64_t out_ld, int64_t out_stride, void* workspace,
                         size_t workspace_bytes, hipStream_t stream) {
-  std::vector<Problem> prog;
+  std::vector<std::vector<Problem>> progs(1);
   DIONW_TRY(ns_program(kind, batch, r, c, x, xt, r_real, c_real, out, out_transposed, out_ld,
-                       out_stride, workspace, workspace_bytes, prog));
-  for (const Problem& p : prog) DIONW_TRY(launch(p, stream));
-  return kOk;
+                       out_stride, workspace, workspace_bytes, progs[0]));
+  int64_t launches = 0;
+  return walk_groups(progs, true, stream, &launches);
 }
 
 int dionw_newton_schulz_group(int32_t count, const int32_t* kind, const int64_t* batch,
