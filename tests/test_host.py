@@ -185,14 +185,18 @@ def _planned_launches(runs: list[tuple[int, int, int, int]]) -> int:
 def test_grouping_plan() -> None:
     """Which products the grouped call merges, from shapes alone (no GPU needed).
 
-    Llama-3-8B's four runs share their 14 symmetric and 2 syrk products (the
-    Q X products already fill whole rounds alone); the MoE runs' products stay
-    apart (their r = 352 side is not a multiple of 64, and grouping the others
-    would replace better-fitting 128 x 128 tiles); GPT-2's three Gram runs share
-    every product and its square block keeps its own 15.
+    A Gram run alone shares one launch between the independent Q Z and G Z
+    products of its fourth iteration where that pays (17 of 18; not with an
+    r = 352 side, which is not a multiple of 64). Llama-3-8B's four runs share
+    their 14 symmetric and 2 syrk products (the Q X products already fill whole
+    rounds alone); the MoE runs' products stay apart (their r = 352 side, and
+    grouping the others would replace better-fitting 128 x 128 tiles); GPT-2's
+    three Gram runs share every product and its square block keeps its own 15.
     """
     llama = [(0, 64, 1024, 4096), (0, 64, 256, 4096), (0, 64, 3584, 4096), (0, 32, 1024, 14336)]
-    assert [_planned_launches([r]) for r in llama] == [18] * 4
+    assert [_planned_launches([r]) for r in llama] == [17] * 4
+    assert _planned_launches([(0, 28, 576, 1152)]) == 17
+    assert _planned_launches([(0, 64, 352, 2048)]) == 18
     assert _planned_launches(llama) == 24
     assert _planned_launches([(0, 128, 352, 2048), (0, 64, 512, 1408)]) == 36
     gpt2 = [(0, 12, 768, 2304), (0, 12, 768, 768), (0, 12, 768, 3072), (0, 12, 768, 3072)]
