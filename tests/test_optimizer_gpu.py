@@ -252,6 +252,40 @@ def test_runs_split_by_missing_gradients_match_lone_params() -> None:
     assert torch.equal(together[1].detach().cpu(), starts[1])
 
 
+def test_runs_above_the_element_cap_step_like_lone_parameters(monkeypatch) -> None:
+    """A bucket above ``MAX_RUN_ELEMENTS`` steps in runs below the cap, and each
+    parameter gets the step it would get alone (tests/test_optimizer.py:687-728;
+    the exact polar factor pins every other stage to float32 rounding)."""
+    import dionw_amd.optimizer as optimizer_module
+
+    monkeypatch.setattr(dionw_amd._buckets, "newton_schulz_fn", lambda _kind: _exact_polar_bf16)
+    monkeypatch.setattr(optimizer_module, "MAX_RUN_ELEMENTS", 2 * 32 * 48)  # two blocks per run
+    runs: list[int] = []
+    real_step_run = optimizer_module.step_run
+
+    def counted(bucket, positions, group, state):
+        runs.append(len(positions))
+        real_step_run(bucket, positions, group, state)
+
+    monkeypatch.setattr(optimizer_module, "step_run", counted)
+    g = torch.Generator().manual_seed(9)
+    starts = [torch.randn(32, 48, generator=g) * 0.02 for _ in range(4)]
+    bucketed = [nn.Parameter(s.clone().to(DEV)) for s in starts]
+    alone = [nn.Parameter(s.clone().to(DEV)) for s in starts]
+    together = _dion(bucketed, 1.0)
+    separately = [_dion([p], 1.0) for p in alone]
+    for _ in range(3):
+        for ours, ref in zip(bucketed, alone):
+            grad = torch.randn(32, 48, generator=g).to(DEV)
+            ours.grad, ref.grad = grad.clone(), grad.clone()
+        together.step()
+        for opt in separately:
+            opt.step()
+    assert runs[:2] == [2, 2], runs
+    for ours, ref in zip(bucketed, alone):
+        torch.testing.assert_close(ours.detach(), ref.detach(), rtol=1e-5, atol=1e-6)
+
+
 def test_head_split_equals_separate_heads() -> None:
     g = torch.Generator().manual_seed(6)
     start = torch.randn(3 * 64, 128, generator=g) * 0.02
