@@ -49,7 +49,7 @@ def adamw_step(group: dict[str, Any], state: ParamState) -> None:
             init_adamw_state(param, entry)
         grad = param.grad
         if grad is None:
-            raise RuntimeError("an AdamW update holds a parameter without a gradient")
+            raise RuntimeError("every parameter of an AdamW pass needs a gradient")
         if param.dtype != torch.float32:
             raise TypeError(f"the HIP AdamW takes float32 parameters, got {param.dtype}")
         data = param.data

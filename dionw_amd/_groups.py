@@ -157,7 +157,7 @@ class GroupSpec:
 
     def _check_matrix(self, params: Sequence[Tensor]) -> None:
         if not 0.0 < self.fraction <= 1.0:
-            raise ValueError(f"fraction must be in (0, 1], got {self.fraction}")
+            raise ValueError(f"the row fraction {self.fraction} lies outside (0, 1]")
         if self.momentum_form is MomentumForm.NESTEROV and self.fraction < 1.0:
             raise ValueError(
                 f"Nesterov momentum needs every row per step (fraction 1.0), got fraction "

@@ -26,11 +26,11 @@ def _check(grad: Tensor, momentum: Tensor) -> Tensor:
     upcast): float16 and bfloat16 convert to float32 exactly.
     """
     if not (grad.is_contiguous() and momentum.is_contiguous()):
-        raise ValueError("the fused momentum kernels need contiguous tensors")
+        raise ValueError("the momentum kernels take contiguous tensors only")
     if momentum.dtype != torch.float32 or grad.numel() != momentum.numel():
-        raise ValueError("the fused momentum kernels need float32 momentum of the grad's size")
+        raise ValueError("the momentum kernels take a float32 momentum with as many elements as the gradient")
     if not grad.is_floating_point():
-        raise ValueError(f"the fused momentum kernels need a float gradient, got {grad.dtype}")
+        raise ValueError(f"the momentum kernels take a float gradient, not {grad.dtype}")
     if grad.device != momentum.device:
         raise ValueError("grad and momentum must be on the same device")
     return grad if grad.dtype == torch.float32 else grad.to(torch.float32)
@@ -150,7 +150,7 @@ def gemm_nt(
 
 def _symmetric_output(a: Tensor, out: Tensor | None) -> Tensor:
     if a.ndim not in (2, 3):
-        raise ValueError(f"Input tensor must be 2D or 3D, but got {a.ndim}D tensor.")
+        raise ValueError(f"expected a 2-D matrix or a 3-D batch, got {a.ndim} dimensions")
     rows = a.size(-2)
     if out is None:
         return torch.empty((*a.shape[:-1], rows), device=a.device, dtype=a.dtype)
@@ -176,7 +176,7 @@ def ns_line_2(a: Tensor, alpha: float, beta: float, *, out: Tensor | None = None
     computing half the tiles (dtypes as ``ns_line_1``)."""
     rows, cols = a.shape[-2:]
     if rows != cols:
-        raise ValueError(f"Input must be symmetric square matrix, but got shape {a.shape}")
+        raise ValueError(f"expected square (symmetric) matrices, got shape {tuple(a.shape)}")
     out = _symmetric_output(a, out)
     gemm_nt(a, a, d=a, alpha=alpha, beta=beta, out=out, symmetric=True)
     return out

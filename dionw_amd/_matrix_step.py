@@ -97,7 +97,7 @@ def _make_run(bucket: Bucket, positions: list[int] | range) -> _Run:
         param = bucket.params[i]
         grad = param.grad
         if grad is None:
-            raise RuntimeError("a Dion run holds a parameter without a gradient")
+            raise RuntimeError("every parameter of a Dion run needs a gradient")
         # Channels-last (or otherwise strided) tensors go through row-major copies.
         grads.append(grad.to(torch.float32).contiguous())
         if param.is_contiguous():

@@ -33,18 +33,18 @@ def swap_plan(model: nn.Module | None, managed: Sequence[nn.Parameter],
         RuntimeError: If only some of the chosen parameters have shadows.
     """
     if not managed:
-        raise ValueError("No parameters available to swap with EMA weights")
+        raise ValueError("No parameters to swap: the optimizer holds no trainable ones")
     chosen: Sequence[nn.Parameter] = managed
     if model is not None:
         ids = {id(p) for p in managed}
         inside = [p for p in model.parameters() if id(p) in ids]
         strangers = [p for p in model.parameters() if id(p) not in ids and p.requires_grad]
         if strangers:
-            raise ValueError(f"{context} EMA swap received a model with {len(strangers)} "
-                             "trainable parameters outside the optimizer.")
+            raise ValueError(f"{context}: {len(strangers)} trainable parameters of the model "
+                             "given to the EMA swap lie outside the optimizer")
         if not inside:
-            raise ValueError(f"{context} EMA swap received a model with no optimizer-managed "
-                             "parameters.")
+            raise ValueError(f"{context}: the model given to the EMA swap has no "
+                             "optimizer-managed parameters")
         chosen = inside
     pairs = []
     for param in chosen:
@@ -52,11 +52,11 @@ def swap_plan(model: nn.Module | None, managed: Sequence[nn.Parameter],
         if shadow is None:
             continue
         if not isinstance(shadow, Tensor):
-            raise TypeError(f"{context} EMA shadow must be a torch.Tensor")
+            raise TypeError(f"{context}: a stored EMA shadow is not a tensor")
         pairs.append((param, shadow))
     if pairs and len(pairs) != len(chosen):
-        raise RuntimeError(f"{context} EMA swap found {len(pairs)} initialized shadows for "
-                           f"{len(chosen)} parameters. Refusing to mix live and EMA weights.")
+        raise RuntimeError(f"{context}: only {len(pairs)} of {len(chosen)} parameters have an "
+                           "initialized shadow; a partial swap would mix live and EMA weights")
     return pairs
 
 
@@ -79,7 +79,7 @@ class WeightSwap:
             RuntimeError: If a swap is already active.
         """
         if self._held:
-            raise RuntimeError("EMA weights are already swapped in")
+            raise RuntimeError("the EMA weights are already swapped in; restore the live weights first")
         for param, shadow in pairs:
             self._held[id(param)] = (param, param.data.clone())
             param.data.copy_(shadow.to(device=param.device, dtype=param.dtype))

@@ -83,19 +83,19 @@ class EMAConfig:
 
     def __post_init__(self) -> None:
         problems = [
-            (self.update_every_n_steps <= 0, "update_every_n_steps must be positive"),
-            (self.start_step < 0, "start_step must be non-negative"),
+            (self.update_every_n_steps <= 0, "update_every_n_steps must be 1 or more"),
+            (self.start_step < 0, "start_step cannot be negative"),
             (not _in_unit_interval(self.decay), "decay must be in [0, 1)"),
             ((self.decay_final is None) != (self.decay_ramp_steps is None),
-             "decay_final and decay_ramp_steps must be set together"),
+             "decay_final and decay_ramp_steps go together: give both or neither"),
             (self.decay_final is not None and not _in_unit_interval(self.decay_final),
              "decay_final must be in [0, 1)"),
             (self.decay_ramp_steps is not None and self.decay_ramp_steps <= 0,
-             "decay_ramp_steps must be positive"),
+             "decay_ramp_steps must be 1 or more"),
             (self.power_gamma is not None and self.decay_final is not None,
-             "power_gamma and the decay_final ramp are exclusive"),
+             "a power schedule (power_gamma) and a linear ramp (decay_final) are mutually exclusive"),
             (self.power_gamma is not None and not self.power_gamma > 0.0,
-             "power_gamma must be positive"),
+             "power_gamma must be positive (above zero)"),
         ]
         for failed, message in problems:
             if failed:
@@ -119,7 +119,7 @@ class EMAConfig:
             ValueError: For a negative ``step_count``.
         """
         if step_count < 0:
-            raise ValueError("step_count must be non-negative")
+            raise ValueError("decay_at_step needs a step count of zero or more")
         kind = self.schedule
         if kind is EMASchedule.CONSTANT:
             return self.decay

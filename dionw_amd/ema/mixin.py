@@ -63,7 +63,7 @@ class IntegratedEMAOptimizer(Optimizer):
             ValueError: If the optimizer has no trainable parameter.
         """
         if not self._trainable():
-            raise ValueError(f"{type(self).__name__} requires at least one trainable parameter")
+            raise ValueError(f"{type(self).__name__} has no parameter that requires a gradient")
         self._ema_helper = None if ema is None else OptimizerIntegratedEMA(self, ema,
                                                                             profile_region)
         self._weight_swap = WeightSwap()
@@ -73,7 +73,7 @@ class IntegratedEMAOptimizer(Optimizer):
 
     @property
     def ema(self) -> OptimizerIntegratedEMA | None:
-        """The EMA, or None when disabled."""
+        """The attached EMA tracker; None for an optimizer built without EMA."""
         return self._ema_helper
 
     @contextmanager
@@ -87,8 +87,8 @@ class IntegratedEMAOptimizer(Optimizer):
             RuntimeError: While EMA weights are swapped in.
         """
         if self._weight_swap.active:
-            raise RuntimeError("step() while EMA weights are swapped in: call "
-                               "restore_non_ema_weights() first")
+            raise RuntimeError("cannot step while the EMA weights are swapped in; call "
+                               "restore_non_ema_weights() before stepping")
         helper = self._ema_helper
         if helper is not None:
             helper.begin_step()
@@ -129,16 +129,16 @@ class IntegratedEMAOptimizer(Optimizer):
         if helper is None:
             if _carries_ema(state_dict):
                 raise ValueError(
-                    f"Checkpoint {name} state carries EMA shadows but the optimizer was built "
-                    "without EMA (ema=None). Build it with the saved EMAConfig to continue the "
-                    "EMA, or load a fresh optimizer state without the EMA.")
+                    f"this {name} checkpoint holds EMA shadows, but the optimizer was built "
+                    "without EMA (ema=None): pass the EMAConfig it was saved with, or load a "
+                    "state saved without an EMA")
             super().load_state_dict(state_dict)
             return
         helper.flush_pending_updates()
         core, count = _split_ema(state_dict)
         if type(count) is not int or count < 0:
-            raise ValueError(f"{name} state has no valid EMA step count "
-                             f"({EMA_STEP_COUNT_KEY}={count!r}): it was not saved with an EMA")
+            raise ValueError(f"this {name} checkpoint was saved without an EMA: its "
+                             f"{EMA_STEP_COUNT_KEY} is {count!r}, not a count of zero or more")
         super().load_state_dict(core)
         for saved_group, group in zip(state_dict["param_groups"], self.param_groups, strict=True):
             for index, param in zip(saved_group["params"], group["params"], strict=True):
@@ -149,7 +149,7 @@ class IntegratedEMAOptimizer(Optimizer):
 
     @property
     def ema_weights_swapped(self) -> bool:
-        """Whether ``swap_ema_weights`` holds EMA weights in the parameters."""
+        """True between ``swap_ema_weights`` and ``restore_non_ema_weights``."""
         return self._weight_swap.active
 
     @torch.no_grad()
@@ -174,7 +174,7 @@ class IntegratedEMAOptimizer(Optimizer):
         if helper is None:
             return False
         if self._weight_swap.active:
-            raise RuntimeError("EMA weights are already swapped in")
+            raise RuntimeError("the EMA weights are already swapped in; restore the live weights first")
         helper.flush_pending_updates()
         pairs = swap_plan(model, self._trainable(), self.state, type(self).__name__)
         return self._weight_swap.apply(pairs)

@@ -119,7 +119,7 @@ class OptimizerIntegratedEMA:
     @step_count.setter
     def step_count(self, value: int) -> None:
         if value < 0:
-            raise ValueError(f"the EMA step count must be non-negative, got {value}")
+            raise ValueError(f"the EMA step count must be non-negative (zero or more), not {value}")
         self._count = value
 
     @property
@@ -215,7 +215,7 @@ class OptimizerIntegratedEMA:
             TypeError: If ``saved`` is not a tensor.
         """
         if not isinstance(saved, Tensor):
-            raise TypeError(f"{type(self.optimizer).__name__} EMA shadow must be a tensor")
+            raise TypeError(f"a saved {type(self.optimizer).__name__} EMA shadow is not a tensor")
         self._place(param, self.optimizer.state[param], saved, bool(initialized))
 
     @torch.no_grad()
@@ -298,7 +298,7 @@ class OptimizerIntegratedEMA:
             self._host.submit(batch, self._lerp_decay())
 
     def flush_pending_updates(self) -> None:
-        """Finish queued EMA work before the shadows are read.
+        """Complete the EMA work still queued, so that the shadows can be read.
 
         Raises:
             RuntimeError: If the CPU worker failed.

@@ -18,7 +18,7 @@ __all__ = ["DION3_UPDATE", "MUON_UPDATE", "MatrixUpdate", "MomentumForm", "RowNo
 
 
 class RowNormalization(Enum):
-    """What a matrix step does to the orthogonalized rows."""
+    """Post-processing of the orthogonalized rows before they are applied."""
 
     NORMUON = "normuon"  # divide rows by the root of an EMA of their mean square
     NONE = "none"        # use the orthogonalized update as is
@@ -33,7 +33,7 @@ class MomentumForm(Enum):
 
 @dataclass(frozen=True)
 class MatrixUpdate:
-    """How a matrix step turns momentum into an update."""
+    """The three choices that define a matrix update: iteration, row scaling, momentum."""
 
     newton_schulz: NewtonSchulz
     row_normalization: RowNormalization

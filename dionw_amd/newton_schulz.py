@@ -46,7 +46,7 @@ _INPUT_ELEMS = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 
 class NewtonSchulz(Enum):
-    """The orthogonalization of matrix updates."""
+    """The Newton-Schulz iteration (and its rounding variant) that orthogonalizes an update."""
 
     POLAR_EXPRESS = "polar_express"
     POLAR_EXPRESS_TRITON = "polar_express_triton"

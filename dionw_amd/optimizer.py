@@ -151,7 +151,7 @@ class Dion(IntegratedEMAOptimizer):
         """
         given = param_group["params"]
         if isinstance(given, set):
-            raise TypeError("Dion param group params must be ordered, not a set")
+            raise TypeError("a Dion param group lists its params in order (a list or tuple), not as a set")
         params = [given] if isinstance(given, Tensor) else list(given)
         for param in params:
             check_parameter(param)

@@ -45,9 +45,9 @@ class _Router:
     def __init__(self, model: nn.Module, *, fraction: float, selection_min_dim: int,
                  min_matrix_dim: int, routes: Mapping[Tensor, Route] | None) -> None:
         if not 0.0 < fraction <= 1.0:
-            raise ValueError(f"fraction must be in (0, 1], got {fraction}")
+            raise ValueError(f"the row fraction {fraction} lies outside (0, 1]")
         if selection_min_dim <= 0 or min_matrix_dim <= 0:
-            raise ValueError("selection_min_dim and min_matrix_dim must be positive")
+            raise ValueError("selection_min_dim and min_matrix_dim must be at least 1")
         self.fraction = fraction
         self.selection_min_dim = selection_min_dim
         self.min_matrix_dim = min_matrix_dim
@@ -66,12 +66,12 @@ class _Router:
         declared: dict[int, Route] = {}
         for source, param, route in claims:
             if id(param) not in self.sites:
-                raise ValueError(f"{source} declares a route for a parameter (shape "
-                                 f"{tuple(param.shape)}) that is not registered on the model")
+                raise ValueError(f"{source} routes a parameter of shape {tuple(param.shape)} "
+                                 "that the model has not registered")
             known = declared.get(id(param))
             if known is not None and known != route:
-                raise ValueError(f"Conflicting routes for a parameter of shape "
-                                 f"{tuple(param.shape)}: {known} vs {route} ({source})")
+                raise ValueError(f"Conflicting routes: {known} and {route} ({source}) both "
+                                 f"claim the parameter of shape {tuple(param.shape)}")
             declared[id(param)] = route
         return declared
 
@@ -164,7 +164,7 @@ def param_groups(
         raise ValueError("No parameters require gradients")
     outside = [tuple(p.shape) for p in chosen if id(p) not in router.sites]
     if outside:
-        raise ValueError(f"Parameters not registered on the model: {outside[:8]}")
+        raise ValueError(f"{len(outside)} of the given parameters are not registered on the model, for instance shapes {outside[:8]}")
     exempt = ({id(p) for p in chosen if decay_exempt(router.sites[id(p)], p)}
               if no_weight_decay is None else {id(p) for p in no_weight_decay})
     decisions = [router.decide(p, id(p) not in exempt) for p in chosen]

@@ -12,7 +12,7 @@ __all__ = ["RouteReason", "RoutedParameter", "RoutingReport"]
 
 
 class RouteReason(Enum):
-    """Why a parameter took its route."""
+    """The rule of the default routing (or a declaration) that chose a route."""
 
     DECLARED = "declared"
     EMBEDDING = "embedding"
@@ -39,7 +39,7 @@ class RoutedParameter:
 
 @dataclass(frozen=True)
 class RoutingReport:
-    """Every routed parameter, in group order."""
+    """One entry per routed parameter, ordered as the groups list them."""
 
     parameters: tuple[RoutedParameter, ...]
 

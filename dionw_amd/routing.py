@@ -18,7 +18,7 @@ __all__ = ["Route", "RouteKind", "RouteProvider"]
 
 
 class RouteKind(Enum):
-    """Which update a parameter receives."""
+    """The two updates a parameter can get: Dion on a matrix, or AdamW."""
 
     ADAMW = "adamw"    # element-wise AdamW
     MATRIX = "matrix"  # the orthogonalized, row-selected matrix update
@@ -46,12 +46,12 @@ class Route:
     def __post_init__(self) -> None:
         if self.kind is RouteKind.ADAMW:
             if self.num_heads is not None or self.fraction is not None:
-                raise ValueError("Route num_heads and fraction apply only to MATRIX routes")
+                raise ValueError("num_heads and fraction are options of MATRIX routes, not of AdamW ones")
         elif self.kind is RouteKind.MATRIX:
             if self.num_heads is not None and self.num_heads <= 0:
-                raise ValueError(f"Route num_heads must be positive, got {self.num_heads}")
+                raise ValueError(f"a route splits into at least one head, not {self.num_heads}")
             if self.fraction is not None and not 0.0 < self.fraction <= 1.0:
-                raise ValueError(f"Route fraction must be in (0, 1], got {self.fraction}")
+                raise ValueError(f"a route's row fraction {self.fraction} lies outside (0, 1]")
         else:
             raise RuntimeError(f"Unhandled RouteKind: {self.kind}")
 
@@ -61,5 +61,5 @@ class RouteProvider(Protocol):
     """A module declaring routes for some of its own parameters."""
 
     def dion_routes(self) -> Iterable[tuple[Tensor, Route]]:
-        """(parameter, route) pairs overriding the default rule."""
+        """Each parameter this module routes itself, with its route."""
         ...

@@ -122,7 +122,7 @@ def test_swap_plan_and_weight_swap() -> None:
     swap.undo()
     assert not swap.active and torch.equal(a.data, torch.ones(3))
     assert swap_plan(None, [a], {}, "Dion") == []  # before the first update
-    with pytest.raises(RuntimeError, match="Refusing to mix"):
+    with pytest.raises(RuntimeError, match="mix live and EMA weights"):
         swap_plan(None, [a, b], {a: state[a]}, "Dion")
     with pytest.raises(ValueError, match="outside the optimizer"):
         swap_plan(nn.Linear(2, 2), [a, b], state, "Dion")
