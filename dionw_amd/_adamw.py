@@ -23,16 +23,19 @@ __all__ = ["adamw_step", "init_adamw_state"]
 
 def init_adamw_state(param: Tensor, state: dict[str, Any]) -> None:
     """Fresh AdamW moments and step counter in ``state``."""
-    state[EXP_AVG_STATE] = torch.zeros_like(param)
-    state[EXP_AVG_SQ_STATE] = torch.zeros_like(param)
-    state[ADAMW_STEP_STATE] = torch.zeros((), dtype=torch.float32, device=param.device)
+    state.update({
+        EXP_AVG_STATE: torch.zeros_like(param),
+        EXP_AVG_SQ_STATE: torch.zeros_like(param),
+        # a 0-d float32 tensor on the parameter's device, as torch's fused AdamW takes it
+        ADAMW_STEP_STATE: param.new_zeros((), dtype=torch.float32),
+    })
 
 
 def adamw_step(group: dict[str, Any], state: ParamState) -> None:
     """One AdamW step of the group's parameters that have gradients.
 
     Raises:
-        RuntimeError: If a gradient disappears between selection and the step.
+        RuntimeError: If a parameter chosen for the pass has lost its gradient.
         TypeError: For a parameter that is not float32.
     """
     params = [p for p in group["params"] if p.grad is not None]

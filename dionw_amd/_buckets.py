@@ -40,9 +40,9 @@ class Bucket:
     """Same-shape blocks of one param group and their packed state.
 
     Attributes:
-        group_index: Index of the owning param group.
+        group_index: Position of the param group the blocks belong to.
         orthogonalize: The group's orthogonalization.
-        params: The bucket's parameters, in group order.
+        params: Parameters with blocks in the bucket, ordered as in their group.
         offsets: First block of each parameter, then the block count.
         rows, cols: Shape of one block.
         selected_rows: Rows updated per step, ``min(rows, ceil(fraction * rows))``.

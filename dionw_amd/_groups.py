@@ -20,7 +20,6 @@ quoted name of a structural key that differs.
 
 from __future__ import annotations
 
-import math
 from collections.abc import Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any, Final
@@ -62,14 +61,14 @@ def matrix_blocks(param: Tensor, num_heads: int | None) -> tuple[int, int, int]:
     columns and a head split divides the rows into ``num_heads`` blocks.
 
     Raises:
-        ValueError: If ``num_heads`` does not divide the rows.
+        ValueError: For a head count that leaves a remainder of rows.
     """
-    rows, cols = int(param.shape[0]), math.prod(int(d) for d in param.shape[1:])
-    if num_heads is None:
-        return 1, rows, cols
-    if rows % num_heads:
-        raise ValueError(f"num_heads={num_heads} does not divide {rows} rows")
-    return num_heads, rows // num_heads, cols
+    rows = int(param.shape[0])
+    cols = int(param.shape[1:].numel())  # trailing dims flattened
+    heads = 1 if num_heads is None else num_heads
+    if rows % heads:
+        raise ValueError(f"{heads} heads: the count does not divide the {rows} rows")
+    return heads, rows // heads, cols
 
 
 def check_decays(*, lr: float, weight_decay: float, eps: float,
@@ -86,7 +85,7 @@ def check_decays(*, lr: float, weight_decay: float, eps: float,
     bad = [(name, v) for name, v in decays.items() if not 0.0 <= v < 1.0]
     if bad:
         name, value = bad[0]
-        raise ValueError(f"{name} must be in [0, 1), got {value}")
+        raise ValueError(f"{name} = {value} lies outside [0, 1)")
 
 
 def check_parameter(param: Tensor) -> None:

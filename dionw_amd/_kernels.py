@@ -37,7 +37,8 @@ def _check(grad: Tensor, momentum: Tensor) -> Tensor:
 
 
 def accumulate_row_l1(grad: Tensor, momentum: Tensor, scores: Tensor, cols: int) -> None:
-    """``momentum += grad``; ``scores[i]`` = l1 norm of momentum row ``i``.
+    """Adds ``grad`` into ``momentum`` and writes each row's sum of absolute
+    values into ``scores``.
 
     Raises:
         ValueError: For non-contiguous tensors, a non-float32 momentum or a
@@ -56,7 +57,8 @@ def accumulate_row_l1(grad: Tensor, momentum: Tensor, scores: Tensor, cols: int)
 def accumulate_copy_decay(
     grad: Tensor, momentum: Tensor, out: Tensor, decay: float, *, nesterov: bool
 ) -> None:
-    """``momentum = decay * (momentum + grad)``; ``out`` = the Newton-Schulz input.
+    """Writes the Newton-Schulz input to ``out`` and leaves the decayed sum
+    ``decay * (momentum + grad)`` in ``momentum``.
 
     ``out`` is ``momentum + grad`` before the decay, or with ``nesterov``
     ``grad`` plus the decayed momentum.
@@ -148,14 +150,15 @@ def gemm_nt(
     return out
 
 
-def _symmetric_output(a: Tensor, out: Tensor | None) -> Tensor:
+def _square_out(a: Tensor, out: Tensor | None) -> Tensor:
     if a.ndim not in (2, 3):
         raise ValueError(f"expected a 2-D matrix or a 3-D batch, got {a.ndim} dimensions")
     rows = a.size(-2)
     if out is None:
         return torch.empty((*a.shape[:-1], rows), device=a.device, dtype=a.dtype)
     if tuple(out.shape) != (*a.shape[:-1], rows):
-        raise ValueError(f"Output must be [..., {rows}, {rows}], got {out.shape}")
+        raise ValueError(f"out has shape {tuple(out.shape)}; the product needs "
+                         f"{(*a.shape[:-1], rows)}")
     return out
 
 
@@ -166,7 +169,7 @@ def ns_line_1(a: Tensor, *, out: Tensor | None = None) -> Tensor:
     output in a's dtype); float32 on the float32 MFMA (the reference's "ieee"
     precision for float32 inputs).
     """
-    out = _symmetric_output(a, out)
+    out = _square_out(a, out)
     gemm_nt(a, a, out=out, symmetric=True)
     return out
 
@@ -177,6 +180,6 @@ def ns_line_2(a: Tensor, alpha: float, beta: float, *, out: Tensor | None = None
     rows, cols = a.shape[-2:]
     if rows != cols:
         raise ValueError(f"expected square (symmetric) matrices, got shape {tuple(a.shape)}")
-    out = _symmetric_output(a, out)
+    out = _square_out(a, out)
     gemm_nt(a, a, d=a, alpha=alpha, beta=beta, out=out, symmetric=True)
     return out

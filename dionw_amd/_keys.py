@@ -2,7 +2,7 @@
 
 These strings are the checkpoint contract of the reference (src/dionw/_keys.py:
 33-68): a state dict saved by either implementation loads in the other.
-torch's own group keys (``params``, ``lr``, ``betas``, ``eps``,
+the group keys torch itself uses (``params``, ``lr``, ``betas``, ``eps``,
 ``weight_decay``) keep torch's spelling.
 """
 

@@ -1,4 +1,4 @@
-"""One Dion step for a run of consecutive bucket parameters with gradients.
+"""The Dion update of a run: consecutive parameters of a bucket that all have gradients.
 
 Reference: src/dionw/_matrix_step.py:104-311. Per block:
 
@@ -114,10 +114,11 @@ def _make_run(bucket: Bucket, positions: list[int] | range) -> _Run:
 def _step_size(bucket: Bucket, lr: float) -> float:
     """lr times AdamW's update RMS times the Frobenius compensation of a
     partial-row step (_matrix_step.py:147-159)."""
-    rows, cols, k = bucket.rows, bucket.cols, bucket.selected_rows
-    return lr * ADAMW_UPDATE_RMS * math.sqrt(max(rows, cols)) * math.sqrt(
-        min(rows, cols) / min(k, cols)
-    )
+    long_side = max(bucket.rows, bucket.cols)
+    short_side = min(bucket.rows, bucket.cols)
+    updated_short_side = min(bucket.selected_rows, bucket.cols)
+    # The reference's order of evaluation, so that the float32 step is the same.
+    return lr * ADAMW_UPDATE_RMS * math.sqrt(long_side) * math.sqrt(short_side / updated_short_side)
 
 
 # Dion.step sets this around its bucket loop: step_run then queues each fused
@@ -193,7 +194,7 @@ def step_run(
     finished when the step's queue is flushed.
 
     Raises:
-        RuntimeError: If a parameter has no gradient.
+        RuntimeError: If a parameter of the run lacks a gradient.
     """
     del state  # the run's momentum and variance are views of the bucket
     run = _make_run(bucket, positions)
@@ -294,7 +295,7 @@ def _finish_run(
         case RowNormalization.NONE:
             pass
         case _ as unreachable:
-            raise RuntimeError(f"Unhandled RowNormalization: {unreachable}")
+            raise RuntimeError(f"no row normalization named {unreachable}")
 
     weight_decay = float(group["weight_decay"])
     decay = 1.0 - lr * weight_decay

@@ -1,4 +1,4 @@
-"""Optimizer-integrated EMA of the parameters, on the GPU or the CPU.
+"""An exponential moving average of the parameters kept by the optimizer (GPU or CPU shadows).
 
 Reference: src/dionw/ema/__init__.py. Shadows live in ``optimizer.state[p]``
 (``ema_shadow``, float32); the schedule position is the top-level

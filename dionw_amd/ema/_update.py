@@ -57,10 +57,10 @@ def foreach_ema_update_(shadows: list[Tensor], sources: list[Tensor], *, decay: 
 
     Raises:
         TypeError: If a shadow is not float32.
-        ValueError: If the lists differ in length.
+        ValueError: If there are more shadows than sources or the other way round.
     """
     if any(shadow.dtype != FP32 for shadow in shadows):
-        raise TypeError("EMA shadows must be float32")
+        raise TypeError("every EMA shadow is kept in float32")
     if len(shadows) != len(sources):
         raise ValueError("shadows and sources differ in length")
     weight = 1.0 - decay

@@ -84,7 +84,7 @@ class IntegratedEMAOptimizer(Optimizer):
         move on the global cadence.
 
         Raises:
-            RuntimeError: While EMA weights are swapped in.
+            RuntimeError: If the EMA weights are in the parameters.
         """
         if self._weight_swap.active:
             raise RuntimeError("cannot step while the EMA weights are swapped in; call "
@@ -166,7 +166,7 @@ class IntegratedEMAOptimizer(Optimizer):
             update).
 
         Raises:
-            RuntimeError: If EMA weights are already swapped in.
+            RuntimeError: If the EMA weights are in the parameters already.
             ValueError: Without parameters to swap, or for a ``model`` that
                 shares none with the optimizer or has trainable ones outside it.
         """

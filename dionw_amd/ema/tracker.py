@@ -80,15 +80,15 @@ def cadence_at(config: EMAConfig, step_count: int) -> Cadence:
 def _pinned_like(param: Tensor, *, pin: bool) -> Tensor:
     """A zeroed host buffer for a parameter's snapshot (float32 and bfloat16
     kept, other dtypes staged as float32)."""
-    dtype = param.dtype if param.dtype in (FP32, torch.bfloat16) else FP32
-    return torch.zeros_like(param, dtype=dtype, device="cpu", pin_memory=pin)
+    staged = param.dtype if param.dtype in (FP32, torch.bfloat16) else FP32
+    return torch.zeros(tuple(param.shape), dtype=staged, device="cpu", pin_memory=pin)
 
 
 class OptimizerIntegratedEMA:
     """EMA shadows stored in an optimizer's per-parameter state.
 
     Attributes:
-        optimizer: The optimizer whose state holds the shadows.
+        optimizer: Owner of the per-parameter state the shadows live in.
         config: Schedule and placement.
     """
 

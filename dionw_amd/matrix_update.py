@@ -1,4 +1,4 @@
-"""The matrix update: orthogonalization, row normalization, momentum form.
+"""Options of the Dion update of a matrix: which iteration, which row scaling, which momentum.
 
 Reference: src/dionw/matrix_update.py:26-73. ``DION3_UPDATE`` (the default) is
 row-selected NorMuon with heavy-ball momentum; ``MUON_UPDATE`` is Keller

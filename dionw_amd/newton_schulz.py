@@ -1,4 +1,4 @@
-"""The orthogonalization of Dion's matrix updates (``NewtonSchulz``).
+"""Newton-Schulz orthogonalization of the matrix updates (``NewtonSchulz`` kinds on HIP kernels).
 
 Reference: src/dionw/newton_schulz.py:30-68, the plugin boundary. Each kind
 maps a ``[N, rows, cols]`` batch (any float dtype) and the epsilon added to its
@@ -36,7 +36,7 @@ from dionw_amd import _lib, _workspace
 
 __all__ = ["NewtonSchulz", "Orthogonalize", "HipOrthogonalize", "newton_schulz_fn"]
 
-# A batched orthogonalization: ([N, rows, cols] input, epsilon) -> bf16 output.
+# Signature of an orthogonalization: a [N, rows, cols] batch and epsilon in, bf16 batch out.
 Orthogonalize = Callable[[Tensor, float], Tensor]
 
 # Library kinds (include/dionw_hip.h, dionw_newton_schulz).
@@ -125,7 +125,7 @@ class HipOrthogonalize:
         kind: The ``NewtonSchulz`` kind.
         lib_kind: The library's kind code.
         dtype: Iteration dtype (float16 for Gram, bfloat16 for the quintics).
-        norm_safety: Factor on the Frobenius norm before normalizing.
+        norm_safety: The Frobenius norm is scaled by this before the input is divided by it.
     """
 
     kind: NewtonSchulz

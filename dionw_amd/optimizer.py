@@ -110,7 +110,7 @@ class Dion(IntegratedEMAOptimizer):
         """Create the optimizer.
 
         Raises:
-            TypeError: For groups without a route or non-float32 parameters.
+            TypeError: For a group without a route, or parameters that are not float32.
             ValueError: For out-of-range hyperparameters, Nesterov momentum with
                 row selection, or parameters off the GPU.
         """
@@ -169,7 +169,7 @@ class Dion(IntegratedEMAOptimizer):
         """Create a parameter's state before its first step, without updating it.
 
         Raises:
-            ValueError: If ``param`` is not in the optimizer.
+            ValueError: For a parameter that no group of this optimizer holds (not in the optimizer).
         """
         owner = next((g for g in self.param_groups if any(p is param for p in g["params"])),
                      None)
@@ -203,7 +203,7 @@ class Dion(IntegratedEMAOptimizer):
         """Update every parameter with a gradient; then the due EMA update.
 
         Raises:
-            RuntimeError: While EMA weights are swapped in.
+            RuntimeError: If the EMA weights are in the parameters.
         """
         with self._ema_cadence():
             loss = None
