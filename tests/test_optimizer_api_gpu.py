@@ -59,29 +59,31 @@ def _rand(shape, gen: torch.Generator) -> Tensor:
 
 
 class _Tiny(nn.Module):
-    """Every route: an embedding, a head-split qkv, a conv, an MLP, a norm, a
-    token parameter and a small head."""
+    """A small model touching every route: an embedding, a fused q/k/v split
+    into heads, a conv, a feed-forward pair, a norm, a learned token and a
+    narrow output."""
 
     def __init__(self) -> None:
         super().__init__()
-        self.embed = nn.Embedding(16, 64)
-        self.qkv = nn.Linear(64, 192)
-        self.conv = nn.Conv1d(64, 64, 3, padding=1)
-        self.up = nn.Linear(64, 128)
-        self.down = nn.Linear(128, 64)
-        self.norm = nn.LayerNorm(64)
-        self.head = nn.Linear(64, 4)
-        self.cls_token = nn.Parameter(torch.zeros(1, 1, 64))
+        self.embed = nn.Embedding(16, 48)
+        self.qkv = nn.Linear(48, 144)
+        self.mix = nn.Conv1d(48, 48, 5, padding=2)
+        self.ff_in = nn.Linear(48, 96)
+        self.ff_out = nn.Linear(96, 48)
+        self.ln = nn.LayerNorm(48)
+        self.out = nn.Linear(48, 4)
+        self.cls_token = nn.Parameter(torch.zeros(1, 1, 48))
 
     def dion_routes(self):
-        return ((self.qkv.weight, Route(RouteKind.MATRIX, num_heads=12, fraction=None)),)
+        yield self.qkv.weight, Route(RouteKind.MATRIX, num_heads=12)
 
     def forward(self, ids: Tensor) -> Tensor:
-        h = self.embed(ids) + self.cls_token
-        h = h + self.qkv(h)[..., :64]
-        h = h + self.conv(h.transpose(1, 2)).transpose(1, 2)
-        h = h + self.down(torch.relu(self.up(self.norm(h))))
-        return self.head(h)
+        x = self.embed(ids) + self.cls_token
+        q, k, v = self.qkv(x).chunk(3, dim=-1)
+        x = x + q * torch.sigmoid(k) + 0.1 * v
+        x = x + self.mix(x.mT).mT
+        x = x + self.ff_out(nn.functional.gelu(self.ff_in(self.ln(x))))
+        return self.out(x)
 
 
 def _tiny_dion(model: nn.Module, lr: float, kind: NewtonSchulz) -> Dion:
