@@ -319,3 +319,17 @@ def test_structural_key_refusal() -> None:
     with pytest.raises(ValueError, match="'newton_schulz'"):
         refuse_structural_change([{"dion_route": "matrix", "fraction": 0.25, "num_heads": None}],
                                  current)
+
+
+def test_integration_example_binds_the_header_signature() -> None:
+    """The ctypes binding shown to maintainers declares as many arguments as the
+    header's declaration of the same entry point."""
+    import re
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    doc = (root / "INTEGRATION.md").read_text()
+    header = (root / "include" / "dionw_hip.h").read_text()
+    name, argtypes = re.search(r"lib\.(dionw_\w+)\.argtypes = \[(.*?)\]", doc, re.S).groups()
+    declared = re.search(rf"\b{name}\((.*?)\);", header, re.S).group(1)
+    assert argtypes.count("ctypes.") == declared.count(",") + 1
