@@ -332,4 +332,8 @@ def test_integration_example_binds_the_header_signature() -> None:
     header = (root / "include" / "dionw_hip.h").read_text()
     name, argtypes = re.search(r"lib\.(dionw_\w+)\.argtypes = \[(.*?)\]", doc, re.S).groups()
     declared = re.search(rf"\b{name}\((.*?)\);", header, re.S).group(1)
-    assert argtypes.count("ctypes.") == declared.count(",") + 1
+    depth, entries = 0, 1
+    for ch in argtypes.strip().rstrip(","):
+        depth += (ch == "(") - (ch == ")")
+        entries += ch == "," and depth == 0
+    assert entries == declared.count(",") + 1
