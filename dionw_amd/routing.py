@@ -26,7 +26,7 @@ class RouteKind(Enum):
 
 @dataclass(frozen=True)
 class Route:
-    """A parameter's route.
+    """Where one parameter goes (Dion or AdamW) and, for Dion, with which options.
 
     Attributes:
         kind: The update.
