@@ -133,6 +133,58 @@ QUEUE_RUNS: Final[int] = 8
 QUEUE_BYTES: Final[int] = 32 * 2**30
 
 
+def _call_work(call: NewtonSchulzCall) -> float:
+    """The F-convention FLOPs of a Newton-Schulz call (a balance weight)."""
+    r, c = float(call.r_real), float(call.c_real)
+    if call.kind == 0 and c > r:
+        return call.blocks * (6.0 * r * r * c + 23.0 * r ** 3)
+    return call.blocks * (15.0 * r * r * c + 5.0 * r ** 3)
+
+
+def _structure(call: NewtonSchulzCall) -> tuple[int, bool, bool]:
+    """What decides a call's sequence of products: its kind, the Gram iteration
+    (a wide Gram block) or the standard one, and whether the iterate is read as
+    it lies (r a multiple of 32)."""
+    return call.kind, call.kind == 0 and call.c_real > call.r_real, call.r % 32 == 0
+
+
+def _lanes(calls: list[NewtonSchulzCall], grouped: bool) -> list[list[int]]:
+    """The queued calls split over at most two streams, each list in queue order.
+
+    Grouped, calls of one structure share launches, so each structure stays in
+    one lane (the most work on the first); one at a time, the calls are balanced
+    by work. One lane when there is nothing to split.
+    """
+    if len(calls) < 2:
+        return [list(range(len(calls)))]
+    if grouped:
+        classes: dict[tuple[int, bool, bool], list[int]] = {}
+        for i, call in enumerate(calls):
+            classes.setdefault(_structure(call), []).append(i)
+        if len(classes) < 2:
+            return [list(range(len(calls)))]
+        ordered = sorted(classes.values(), key=lambda ix: -sum(_call_work(calls[i]) for i in ix))
+        return [ordered[0], sorted(i for ix in ordered[1:] for i in ix)]
+    lanes: list[list[int]] = [[], []]
+    load = [0.0, 0.0]
+    for i in sorted(range(len(calls)), key=lambda i: -_call_work(calls[i])):
+        lane = 0 if load[0] <= load[1] else 1
+        lanes[lane].append(i)
+        load[lane] += _call_work(calls[i])
+    return [sorted(lane) for lane in lanes if lane]
+
+
+_SIDE_STREAMS: dict[torch.device, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream of ``device`` (default priority) for a lane of Newton-Schulz work."""
+    side = _SIDE_STREAMS.get(device)
+    if side is None:
+        side = _SIDE_STREAMS[device] = torch.cuda.Stream(device)
+    return side
+
+
 class RunQueue:
     """Bucket runs waiting for their Newton-Schulz call and the passes after it."""
 
@@ -141,6 +193,7 @@ class RunQueue:
         self._finish: list[Callable[[], None]] = []
         self._bytes = 0
         self._stream: int | None = None
+        self._device: torch.device | None = None
 
     def slot(self, nbytes: int, stream: int) -> str:
         """Name suffix of the next run's buffers; flushes first if that run does not fit."""
@@ -150,30 +203,54 @@ class RunQueue:
         return f"#{len(self._calls)}"
 
     def add(self, call: NewtonSchulzCall, finish: Callable[[], None], nbytes: int,
-            stream: int) -> None:
+            stream: int, device: torch.device) -> None:
         self._calls.append(call)
         self._finish.append(finish)
         self._bytes += nbytes
         self._stream = stream
+        self._device = device
 
     def flush(self) -> None:
-        """Run the queued Newton-Schulz calls and finish the runs, in queue order.
+        """Run the queued Newton-Schulz calls and finish the runs.
 
-        When grouping saves no launch, each run's iteration is followed by its
-        own passes instead, which then find its output still in cache.
+        The calls go out grouped when that saves launches; then each run's passes
+        follow. When grouping saves no launch, each run's iteration is followed
+        by its own passes instead, which then find its output still in cache.
+        Calls that cannot share launches (different structures, or none grouped)
+        run on two streams, the second joining the first at the end: their
+        products, each a round of tiles or less on small blocks, then fill the
+        CUs together.
         """
         if not self._calls:
             return
-        calls, finish, stream = self._calls, self._finish, self._stream
+        calls, finish, stream, device = self._calls, self._finish, self._stream, self._device
         self._calls, self._finish, self._bytes, self._stream = [], [], 0, None
-        if len(calls) > 1 and group_launches(calls) < sum(group_launches([c]) for c in calls):
-            run_newton_schulz_group(calls, stream)
-            for done in finish:
-                done()
+        grouped = len(calls) > 1 and group_launches(calls) < sum(group_launches([c]) for c in calls)
+        lanes = _lanes(calls, grouped)
+        if len(lanes) == 1:
+            _run_lane(calls, finish, lanes[0], grouped, stream)
             return
-        for call, done in zip(calls, finish):
-            run_newton_schulz_call(call, stream)
-            done()
+        main = torch.cuda.current_stream(device)
+        side = _side_stream(device)
+        side.wait_stream(main)
+        for lane, lane_stream in zip(lanes, (main, side)):
+            with torch.cuda.stream(lane_stream):
+                _run_lane(calls, finish, lane, grouped, lane_stream.cuda_stream)
+        main.wait_stream(side)
+
+
+def _run_lane(calls: list[NewtonSchulzCall], finish: list[Callable[[], None]], lane: list[int],
+              grouped: bool, stream: int) -> None:
+    """The calls ``lane`` of the queue, then (or each followed by) their runs' passes."""
+    mine = [calls[i] for i in lane]
+    if grouped and len(mine) > 1 and group_launches(mine) < sum(group_launches([c]) for c in mine):
+        run_newton_schulz_group(mine, stream)
+        for i in lane:
+            finish[i]()
+        return
+    for i in lane:
+        run_newton_schulz_call(calls[i], stream)
+        finish[i]()
 
 
 def _ns_bytes(ortho: HipOrthogonalize, blocks: int, k: int, cols: int) -> int:
@@ -251,7 +328,7 @@ def step_run(
             call = newton_schulz_call(ortho, blocks, k, cols, xr, xt, orthogonal,
                                       "ns_workspace" + own)
             queue.add(call, partial(_finish_run, run, bucket, positions, group, orthogonal, idx,
-                                    slot, step, stream), nbytes, stream)
+                                    slot, step), nbytes, stream, device)
             return
         run_newton_schulz(ortho, blocks, k, cols, xr, xt, orthogonal, stream)
     else:
@@ -261,7 +338,7 @@ def step_run(
                   _lib.F32, raw.data_ptr(), None, stream)
         orthogonal = ortho(raw, NEWTON_SCHULZ_EPS)
         orthogonal = orthogonal.to(torch.bfloat16).contiguous()
-    _finish_run(run, bucket, positions, group, orthogonal, idx, slot, step, stream)
+    _finish_run(run, bucket, positions, group, orthogonal, idx, slot, step)
 
 
 def _finish_run(
@@ -273,11 +350,12 @@ def _finish_run(
     idx: Tensor | None,
     slot: Tensor | None,
     step: float,
-    stream: int,
 ) -> None:
     """NorMuon statistics and the weight update of a run whose orthogonalized
-    rows ``orthogonal`` ([blocks, k, cols] bf16) are ready (_matrix_step.py:274-311)."""
+    rows ``orthogonal`` ([blocks, k, cols] bf16) are ready (_matrix_step.py:274-311),
+    on torch's current stream (the queue may finish a run on its second stream)."""
     device = run.momentum.device
+    stream = _lib.stream_handle(device)
     blocks, rows, cols, k = run.blocks, bucket.rows, bucket.cols, bucket.selected_rows
     count = len(run.params)
     per_param = bucket.blocks_per_param
