@@ -83,12 +83,20 @@ class Timeline:
         module.call = original
 
     def summary(self) -> dict[str, dict[str, float]]:
+        """Per entry point: calls, algorithmic flops or bytes, and "ms", the time
+        during which at least one of its calls ran. The optimizer may run calls
+        on two streams at once, so their durations are not summed: each call's
+        interval is placed on one clock (the first event's) and the union is
+        measured."""
         self.torch.cuda.synchronize()
         out: dict[str, dict[str, float]] = defaultdict(lambda: {"ms": 0.0, "calls": 0, "flops": 0.0,
                                                                  "bytes": 0.0})
+        spans: dict[str, list[tuple[float, float]]] = defaultdict(list)
+        origin = self.events[0][2] if self.events else None
         for name, meta, start, end in self.events:
+            key = "dionw_newton_schulz" if name == "dionw_newton_schulz_group" else name
+            spans[key].append((origin.elapsed_time(start), origin.elapsed_time(end)))
             entry = out[name]
-            entry["ms"] += start.elapsed_time(end)
             entry["calls"] += 1
             a = meta["args"]
             if name == "dionw_newton_schulz":
@@ -104,7 +112,6 @@ class Timeline:
                 # Reported with the single calls: the same products, grouped.
                 del out[name]
                 entry = out["dionw_newton_schulz"]
-                entry["ms"] += start.elapsed_time(end)
                 entry["calls"] += 1
                 n = a[0]
                 for i in range(n):
@@ -144,6 +151,13 @@ class Timeline:
                 entry["bytes"] += 36.0 * sum(a[6][i] for i in range(a[7]))
             elif name == "dionw_ema_update":
                 entry["bytes"] += (8.0 if a[5] else 12.0) * sum(a[2][i] for i in range(a[3]))
+        for key, intervals in spans.items():
+            covered, reach = 0.0, float("-inf")
+            for begin, finish in sorted(intervals):
+                if finish > reach:
+                    covered += finish - max(begin, reach)
+                    reach = finish
+            out[key]["ms"] = covered
         return dict(out)
 
 
