@@ -1034,11 +1034,15 @@ int64_t wgs_of(const Problem& p, int tile) {
 
 // Rounds of workgroups over the 256 CUs (one 256x256 or two 128x128 per CU),
 // in units of one 256x256 round: a 128x128 round counts 2 * 128^2 / 256^2 *
-// 1.2 (the smaller tile's measured rate on the large shapes is 1/1.2 of the
-// 256x256 tile's).
-// Both in tenths of a 256x256 round (a 128x128 round is exactly 0.6).
-int64_t big_tenths(const Problem& p) { return 10 * ((wgs_of(p, 256) + 255) / 256); }
-int64_t mid_tenths(const Problem& p) { return 6 * ((wgs_of(p, 128) + 511) / 512); }
+// 1.3 (the smaller tile's rate is about 1/1.3 of the 256x256 tile's: with 1.2,
+// MoE-Muon's 1408-row symmetric products took the smaller tile and ran 2.4%
+// slower than on 256x256 tiles, while the MoE products that keep it are faster
+// there).
+// Both in twentieths of a 256x256 round (a 128x128 round is 0.65).
+constexpr int kBigRound = 20, kMidRound = 13;
+constexpr double kMidRate = (double)kMidRound / kBigRound;
+int64_t big_cost(const Problem& p) { return kBigRound * ((wgs_of(p, 256) + 255) / 256); }
+int64_t mid_cost(const Problem& p) { return kMidRound * ((wgs_of(p, 128) + 511) / 512); }
 
 template <typename T, typename OUT_T, int MODE>
 int launch_typed(const Problem& p, hipStream_t stream) {
@@ -1071,7 +1075,7 @@ int launch_typed(const Problem& p, hipStream_t stream) {
 #endif
   if (k32) {
     // The smaller tile wins when the big one leaves CUs idle or pads a ragged side.
-    if (big_tenths(p) <= mid_tenths(p)) {
+    if (big_cost(p) <= mid_cost(p)) {
       if (k64) return launch_pipe<T, OUT_T, MODE, Big64>(p, stream);
       return launch_pipe<T, OUT_T, MODE, Big32>(p, stream);
     }
@@ -1120,7 +1124,9 @@ int launch(const Problem& p, hipStream_t stream) {
 
 // Whether one grouped launch beats one launch per product, and on which tile.
 // Time in 256x256 rounds times k (a round of 256x256 tiles over depth k costs
-// k, a round of two 128x128 tiles per CU 0.6 k). Alone, each product takes its
+// k, a round of two 128x128 tiles per CU kGroupMidRate k: the rate the grouping
+// choices were measured with, e.g. gram-ns's lone-run pair on 128x128 tiles,
+// 1.35 -> 1.32 ms; the launcher's own tile rule counts kMidRate). Alone, each product takes its
 // better tile (the launcher's rule); grouped, the tiles of all of them fill the
 // CUs longest first, which costs their total work over the CUs plus about half
 // a round of the shortest tiles, and no less than the longest tile.
@@ -1134,22 +1140,24 @@ int launch(const Problem& p, hipStream_t stream) {
 // for the runs' positions too measured slower on GPT-2-small's runs, whose
 // products then group on 128x128 tiles.)
 constexpr double kRamp = 340.0;
+constexpr double kGroupMidRate = 0.6;
 
 GroupTile group_plan(const std::vector<const Problem*>& ps, bool pair) {
   const double ramp = pair ? kRamp : 0.0;
   double separate = 0.0, big = 0.0, mid = 0.0, kmax = 0.0, kmin = 1e300;
   for (const Problem* p : ps) {
     const double k = (double)p->g.k;
-    separate += ramp + k * 0.1 * (double)std::min(big_tenths(*p), mid_tenths(*p));
+    separate += ramp + k * (double)std::min(big_cost(*p), mid_cost(*p)) / kBigRound;
     big += k * (double)wgs_of(*p, 256) / 256.0;
-    mid += 0.6 * k * (double)wgs_of(*p, 128) / 512.0;
+    mid += kGroupMidRate * k * (double)wgs_of(*p, 128) / 512.0;
     kmax = std::max(kmax, k);
     kmin = std::min(kmin, k);
   }
-  const double big_cost = ramp + std::max(big + 0.5 * kmin, kmax);
-  const double mid_cost = pair ? ramp + std::max(mid + 0.3 * kmin, 0.6 * kmax) : 1e300;
-  if (std::min(big_cost, mid_cost) >= separate) return kNoGroup;
-  return mid_cost < big_cost ? kGroupMid : kGroupBig;
+  const double big_total = ramp + std::max(big + 0.5 * kmin, kmax);
+  const double mid_total =
+      pair ? ramp + std::max(mid + 0.5 * kGroupMidRate * kmin, kGroupMidRate * kmax) : 1e300;
+  if (std::min(big_total, mid_total) >= separate) return kNoGroup;
+  return mid_total < big_total ? kGroupMid : kGroupBig;
 }
 
 // Independent products in as few launches as possible: one grouped launch when
