@@ -630,14 +630,14 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs& g, int w) {
   const int lrow = lane & 31, lk = lane >> 5;
   // A wave computes nothing when no element of its block is ever stored: in a
   // diagonal tile of a symmetric product, a block wholly below the diagonal
-  // (wm > wn; the epilogue overwrites that part with the mirror of the upper
-  // one), and a block wholly past the stored rows or columns (the padding of a
-  // ragged side). Under the board's power limit the MFMAs saved buy clock for
-  // the rest. The wave still issues its share of the stage loads and takes
-  // every barrier, in a loop of its own (a branch inside the main loop costs the
-  // 4-wave 128x128 kernel registers and time).
+  // (its first row past its last column; the epilogue overwrites that part with
+  // the mirror of the upper one), and a block wholly past the stored rows or
+  // columns (the padding of a ragged side). Under the board's power limit the
+  // MFMAs saved buy clock for the rest. The wave still issues its share of the
+  // stage loads and takes every barrier, in a loop of its own (a branch inside
+  // the main loop costs the 4-wave 128x128 kernel registers and time).
   const bool diag_tile = g.sym && tm == tn;
-  const bool idle = (diag_tile && wm > wn) || m0 + wm * WTM >= g.m_lim ||
+  const bool idle = (diag_tile && wm * WTM >= (wn + 1) * WTN) || m0 + wm * WTM >= g.m_lim ||
                     n0 + wn * WTN >= g.n_lim;
   // Stage kt has landed for every wave; the stage PSTAGES - 1 ahead is issued.
   auto advance = [&](int kt) {
