@@ -152,13 +152,19 @@ class Timeline:
             elif name == "dionw_ema_update":
                 entry["bytes"] += (8.0 if a[5] else 12.0) * sum(a[2][i] for i in range(a[3]))
         for key, intervals in spans.items():
-            covered, reach = 0.0, float("-inf")
-            for begin, finish in sorted(intervals):
-                if finish > reach:
-                    covered += finish - max(begin, reach)
-                    reach = finish
-            out[key]["ms"] = covered
+            out[key]["ms"] = covered_ms(intervals)
         return dict(out)
+
+
+def covered_ms(intervals: list[tuple[float, float]]) -> float:
+    """Length of the union of (begin, end) intervals: the time during which at
+    least one of them was running."""
+    covered, reach = 0.0, float("-inf")
+    for begin, finish in sorted(intervals):
+        if finish > reach:
+            covered += finish - max(begin, reach)
+            reach = finish
+    return covered
 
 
 def build_llama(torch, dev, spec, fraction):

@@ -30,6 +30,15 @@ def test_ns_flops_convention() -> None:
     assert abs(16 * bench.ns_flops(0, 1024, 4096) / 1e12 - 0.8075) < 5e-4
 
 
+def test_phase_time_is_the_union_of_call_intervals() -> None:
+    """Calls on two streams overlap: a phase's time counts each instant once."""
+    assert bench.covered_ms([]) == 0.0
+    assert bench.covered_ms([(0.0, 2.0), (1.0, 3.0), (5.0, 6.0)]) == 4.0
+    assert bench.covered_ms([(0.0, 10.0), (2.0, 3.0)]) == 10.0          # nested
+    assert bench.covered_ms([(4.0, 5.0), (0.0, 1.0), (1.0, 2.0)]) == 3.0  # unsorted, touching
+    assert bench.covered_ms([(1.0, 2.0), (1.0, 2.0)]) == 1.0            # identical
+
+
 def test_ns_algorithmic_bytes() -> None:
     # Writes 18 r^2 + 2 r c, reads 25 r^2 + 4 r c per block (16-bit) when X is
     # read as it lies; a transposed copy adds one r c write.

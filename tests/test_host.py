@@ -182,6 +182,32 @@ def _planned_launches(runs: list[tuple[int, int, int, int]]) -> int:
         arr(i64, rows), arr(i64, cols))
 
 
+def test_queue_lanes() -> None:
+    """How a flush spreads its calls over two streams: calls that share launches
+    (one structure) stay on one lane, the structure with the most work on the
+    first; calls that go out one by one are balanced by work; each lane keeps
+    queue order."""
+    from dionw_amd._matrix_step import _lanes
+    from dionw_amd.newton_schulz import NewtonSchulzCall
+
+    def call(kind, blocks, r, c, r_real=None, c_real=None):
+        return NewtonSchulzCall(kind, blocks, r, c, 0, 0, r_real or r, c_real or c, 0, 0, c, r * c,
+                                0, 0)
+
+    wide = [call(0, 12, 768, 3072), call(0, 12, 768, 2304), call(0, 12, 768, 3072)]
+    square = call(0, 12, 768, 768)
+    # GPT-2 small: three wide Gram runs and the square run's standard iteration.
+    assert _lanes([wide[0], square, wide[1], wide[2]], grouped=True) == [[0, 2, 3], [1]]
+    assert _lanes(wide, grouped=True) == [[0, 1, 2]]      # one structure: one lane
+    assert _lanes([square], grouped=True) == [[0]]
+    # One by one: the biggest call alone, the other two together.
+    big, small = call(0, 64, 1024, 4096), call(0, 32, 1024, 4096)
+    assert _lanes([small, big, small], grouped=False) == [[1], [0, 2]]
+    # A structure whose rows are not a multiple of 32 differs from one whose are.
+    ragged = call(0, 12, 776, 3072, r_real=770)
+    assert len(_lanes([wide[0], ragged], grouped=True)) == 2
+
+
 def test_grouping_plan() -> None:
     """Which products the grouped call merges, from shapes alone (no GPU needed).
 
