@@ -102,6 +102,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [_pp, _pp, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _f32, _f32, _i32, _f32, _p],
     ),
+    "dionw_apply_update_stage": (
+        ctypes.c_int,
+        [_pp, _pp, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _f32, _f32, _i32, _p],
+    ),
     "dionw_increment_steps": (ctypes.c_int, [_pp, _i32, _p]),
     "dionw_adamw": (
         ctypes.c_int,

@@ -384,13 +384,21 @@ def _finish_run(
     # instead of apply then EMA; the same lerp arithmetic).
     ema = ACTIVE_EMA.get()
     params = [bucket.params[i] for i in positions]
-    shadows = ema.fusable_shadows(params) if ema is not None and not run.writeback else None
-    if shadows is None:
-        _lib.call("dionw_apply_update", _lib.ptr_array(run.params), *common, stream)
-    else:
+    fusable = ema is not None and not run.writeback
+    shadows = ema.fusable_shadows(params) if fusable else None
+    # A due CPU EMA's host snapshots may be written by the same pass (the new
+    # weights go to HBM and over the host link at once) instead of copied after it.
+    staged = ema.stageable_buffers(params) if fusable and ema.fuse_host_copies else None
+    if shadows is not None:
         _lib.call("dionw_apply_update_ema", _lib.ptr_array(run.params), _lib.ptr_array(shadows),
                   *common, ema.fused_weight(), stream)
         ema.mark_fused(params)
+    elif staged is not None:
+        _lib.call("dionw_apply_update_stage", _lib.ptr_array(run.params),
+                  _lib.ptr_array(staged), *common, stream)
+        ema.mark_staged(params)
+    else:
+        _lib.call("dionw_apply_update", _lib.ptr_array(run.params), *common, stream)
     for param, copy in run.writeback:
         param.copy_(copy)
     if ema is not None:

@@ -106,8 +106,17 @@ struct ApplyArgs {
   float step, decay;
   int apply_decay, only_selected, vec;
   int64_t rows_per_tensor, rows, cols, k;
-  float* shadow[kMaxTensors];  // EMA shadows laid out like the parameters (fused EMA)
+  // Per parameter, laid out like it: the EMA shadow (kApplyEma) or the pinned
+  // host staging buffer the new weights are also written to (kApplyStage).
+  float* side[kMaxTensors];
   float ema_weight;
+};
+
+// What the apply pass does besides W's update.
+enum ApplyMode : int {
+  kApplyPlain = 0,  // nothing
+  kApplyEma = 1,    // S = lerp(S, W_new) on every row (GPU EMA fused in)
+  kApplyStage = 2,  // every row's W_new also stored to host memory (CPU EMA snapshot)
 };
 
 __device__ __forceinline__ float update_one(float w, float o, float d, float s,
@@ -121,10 +130,14 @@ __device__ __forceinline__ float update_one(float w, float o, float d, float s,
 // faster than a wavefront per row).
 constexpr int kApplyThreads = 256;
 
-// EMA: every row's shadow also moves to the row's new weights (lerp with
+// kApplyEma: every row's shadow also moves to the row's new weights (lerp with
 // ema_weight), also on rows that are only decayed or not changed at all.
-template <bool EMA>
+// kApplyStage: every row's new weights are also stored to the row's place in a
+// pinned host buffer (over the host link; the device copy is not read again).
+template <int Mode>
 __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
+  constexpr bool EMA = Mode == kApplyEma;
+  constexpr bool STAGE = Mode == kApplyStage;
   const int tid = threadIdx.x;
   const int64_t r = blockIdx.x;  // the grid has exactly one workgroup per row
   int64_t gr, slot, b;
@@ -141,28 +154,36 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
   const int tensor = (int)(gr / a.rows_per_tensor);
   const int64_t offset = (gr - (int64_t)tensor * a.rows_per_tensor) * a.cols;
   float* w = a.t.param[tensor] + offset;
-  float* sh = EMA ? a.shadow[tensor] + offset : nullptr;
+  float* sh = (EMA || STAGE) ? a.side[tensor] + offset : nullptr;
   const bool apply_decay = a.apply_decay != 0;
   constexpr int U = 4;  // chunks whose loads are issued together
   constexpr int T = kApplyThreads;
+  // The new weights' other destination: the EMA shadow's lerp or the host copy.
+  auto side4 = [&](f32x4 wv, int64_t c) {
+    f32x4* s4 = reinterpret_cast<f32x4*>(sh);
+    if (EMA) {
+      f32x4 sv = __builtin_nontemporal_load(s4 + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], wv[e], a.ema_weight);
+      __builtin_nontemporal_store(sv, s4 + c);
+    }
+    if (STAGE) s4[c] = wv;
+  };
+  auto side1 = [&](float wv, int64_t c) {
+    if (EMA) sh[c] = ema_lerp(sh[c], wv, a.ema_weight);
+    if (STAGE) sh[c] = wv;
+  };
   // Every element is read once and written once: the vector paths stream
   // (non-temporal loads and stores), which moves this traffic faster.
   if (slot < 0) {
-    if (!apply_decay && !EMA) return;
-    // Rows outside the selection: W = W d (weight decay) and, with the EMA,
-    // S = lerp(S, W).
+    if (!apply_decay && !EMA && !STAGE) return;
+    // Rows outside the selection: W = W d (weight decay), and the side copy.
     auto row_end = [&](f32x4 wv, int64_t c) {
       if (apply_decay) {
         wv = wv * a.decay;
         __builtin_nontemporal_store(wv, reinterpret_cast<f32x4*>(w) + c);
       }
-      if (EMA) {
-        f32x4* s4 = reinterpret_cast<f32x4*>(sh);
-        f32x4 sv = __builtin_nontemporal_load(s4 + c);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], wv[e], a.ema_weight);
-        __builtin_nontemporal_store(sv, s4 + c);
-      }
+      side4(wv, c);
     };
     if (a.vec) {
       const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
@@ -180,7 +201,7 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
       for (int64_t c = tid; c < a.cols; c += T) {
         float wv = w[c];
         if (apply_decay) w[c] = wv = wv * a.decay;
-        if (EMA) sh[c] = ema_lerp(sh[c], wv, a.ema_weight);
+        side1(wv, c);
       }
     }
     return;
@@ -201,13 +222,7 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
     };
     auto store = [&](int64_t c, f32x4 wv) {
       __builtin_nontemporal_store(wv, w4 + c);
-      if (EMA) {
-        f32x4* s4 = reinterpret_cast<f32x4*>(sh);
-        f32x4 sv = __builtin_nontemporal_load(s4 + c);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sv[e] = ema_lerp(sv[e], wv[e], a.ema_weight);
-        __builtin_nontemporal_store(sv, s4 + c);
-      }
+      side4(wv, c);
     };
     const int64_t n4 = a.cols >> 2;
     int64_t c = tid;
@@ -228,13 +243,34 @@ __global__ __launch_bounds__(kApplyThreads) void apply_kernel(ApplyArgs a) {
     for (int64_t c = tid; c < a.cols; c += T) {
       const float wv = update_one(w[c], (float)o[c], d, s, normalized, a.decay, apply_decay);
       w[c] = wv;
-      if (EMA) sh[c] = ema_lerp(sh[c], wv, a.ema_weight);
+      side1(wv, c);
     }
   }
 }
 
-// One launch per kMaxTensors parameters; shadows (may be null) get the fused EMA.
-int apply_launch(float* const* params, float* const* shadows, int32_t count,
+// The device-side address of a host buffer the apply pass writes to: it must be
+// pinned host memory mapped into the device's address space (hipHostMalloc, or
+// torch's pin_memory=True); anything else is rejected before a launch.
+int host_staging_address(float* host, int index, float** device) {
+  DIONW_REQUIRE(host, "apply_update_stage: null host staging buffer %d", index);
+  hipPointerAttribute_t attr{};
+  const hipError_t rc = hipPointerGetAttributes(&attr, host);
+  if (rc != hipSuccess) {
+    (void)hipGetLastError();  // an unknown pointer leaves the error set: clear it
+    set_error("apply_update_stage: host staging buffer %d is not pinned host memory (%s)", index,
+              hipGetErrorString(rc));
+    return kInvalid;
+  }
+  DIONW_REQUIRE(attr.type == hipMemoryTypeHost && attr.devicePointer,
+                "apply_update_stage: host staging buffer %d is not pinned host memory mapped "
+                "for the device (memory type %d)", index, (int)attr.type);
+  *device = static_cast<float*>(attr.devicePointer);
+  return kOk;
+}
+
+// One launch per kMaxTensors parameters. `side` (null for kApplyPlain) holds one
+// buffer per parameter: EMA shadows (kApplyEma) or host staging (kApplyStage).
+int apply_launch(int mode, float* const* params, float* const* side, int32_t count,
                  int64_t blocks_per_tensor, int64_t rows, int64_t cols, int64_t k,
                  const void* orthogonal, const int32_t* idx, const int32_t* slot,
                  const float* rowd, const float* scale, float step, float decay,
@@ -243,6 +279,7 @@ int apply_launch(float* const* params, float* const* shadows, int32_t count,
                     k > 0 && k <= rows,
                 "apply_update: bad arguments");
   DIONW_REQUIRE(k == rows || (idx && slot), "apply_update: row selection needs idx and slot");
+  DIONW_REQUIRE((mode == kApplyPlain) == (side == nullptr), "apply_update: bad side table");
   for (int32_t start = 0; start < count; start += kMaxTensors) {
     ApplyArgs a{};
     a.t.count = (count - start) < kMaxTensors ? (count - start) : kMaxTensors;
@@ -251,11 +288,13 @@ int apply_launch(float* const* params, float* const* shadows, int32_t count,
       DIONW_REQUIRE(params[start + i], "apply_update: null parameter %d", start + i);
       a.t.param[i] = params[start + i];
       aligned = aligned && aligned16(params[start + i]);
-      if (shadows) {
-        DIONW_REQUIRE(shadows[start + i], "apply_update: null EMA shadow %d", start + i);
-        a.shadow[i] = shadows[start + i];
-        aligned = aligned && aligned16(shadows[start + i]);
+      if (mode == kApplyEma) {
+        DIONW_REQUIRE(side[start + i], "apply_update: null EMA shadow %d", start + i);
+        a.side[i] = side[start + i];
+      } else if (mode == kApplyStage) {
+        DIONW_TRY(host_staging_address(side[start + i], start + i, &a.side[i]));
       }
+      if (side) aligned = aligned && aligned16(a.side[i]);
     }
     const int64_t b0 = (int64_t)start * blocks_per_tensor;
     a.o = reinterpret_cast<const __bf16*>(orthogonal) + b0 * k * cols;
@@ -272,17 +311,24 @@ int apply_launch(float* const* params, float* const* shadows, int32_t count,
     a.k = k;
     a.vec = aligned && (reinterpret_cast<uintptr_t>(a.o) & 7) == 0;
     a.ema_weight = ema_weight;
-    // The EMA moves every row's shadow, so every row is visited.
-    a.only_selected = !apply_decay && !shadows && k < rows;
+    // The EMA and the host copy cover every row, so every row is visited.
+    a.only_selected = !apply_decay && mode == kApplyPlain && k < rows;
     const int64_t n = a.only_selected ? (int64_t)a.t.count * blocks_per_tensor * k
                                       : (int64_t)a.t.count * a.rows_per_tensor;
     if (n == 0) continue;
     DIONW_REQUIRE(n * kApplyThreads <= (int64_t)UINT32_MAX,
                   "apply_update: %lld rows exceed one launch", (long long)n);
-    if (shadows)
-      hipLaunchKernelGGL(apply_kernel<true>, dim3((unsigned)n), dim3(kApplyThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL(apply_kernel<false>, dim3((unsigned)n), dim3(kApplyThreads), 0, stream, a);
+    const dim3 grid((unsigned)n), block(kApplyThreads);
+    switch (mode) {
+      case kApplyEma:
+        hipLaunchKernelGGL(apply_kernel<kApplyEma>, grid, block, 0, stream, a);
+        break;
+      case kApplyStage:
+        hipLaunchKernelGGL(apply_kernel<kApplyStage>, grid, block, 0, stream, a);
+        break;
+      default:
+        hipLaunchKernelGGL(apply_kernel<kApplyPlain>, grid, block, 0, stream, a);
+    }
     DIONW_TRY(check_launch("apply_update"));
   }
   return kOk;
@@ -390,8 +436,8 @@ int dionw_apply_update(float* const* params, int32_t count, int64_t blocks_per_t
                        const int32_t* idx, const int32_t* slot, const float* rowd,
                        const float* scale, float step, float decay, int32_t apply_decay,
                        hipStream_t stream) {
-  return apply_launch(params, nullptr, count, blocks_per_tensor, rows, cols, k, orthogonal, idx,
-                      slot, rowd, scale, step, decay, apply_decay, 0.f, stream);
+  return apply_launch(kApplyPlain, params, nullptr, count, blocks_per_tensor, rows, cols, k,
+                      orthogonal, idx, slot, rowd, scale, step, decay, apply_decay, 0.f, stream);
 }
 
 int dionw_apply_update_ema(float* const* params, float* const* shadows, int32_t count,
@@ -400,8 +446,19 @@ int dionw_apply_update_ema(float* const* params, float* const* shadows, int32_t 
                            const float* rowd, const float* scale, float step, float decay,
                            int32_t apply_decay, float ema_weight, hipStream_t stream) {
   DIONW_REQUIRE(shadows, "apply_update_ema: null shadow table");
-  return apply_launch(params, shadows, count, blocks_per_tensor, rows, cols, k, orthogonal, idx,
-                      slot, rowd, scale, step, decay, apply_decay, ema_weight, stream);
+  return apply_launch(kApplyEma, params, shadows, count, blocks_per_tensor, rows, cols, k,
+                      orthogonal, idx, slot, rowd, scale, step, decay, apply_decay, ema_weight,
+                      stream);
+}
+
+int dionw_apply_update_stage(float* const* params, float* const* staged, int32_t count,
+                             int64_t blocks_per_tensor, int64_t rows, int64_t cols, int64_t k,
+                             const void* orthogonal, const int32_t* idx, const int32_t* slot,
+                             const float* rowd, const float* scale, float step, float decay,
+                             int32_t apply_decay, hipStream_t stream) {
+  DIONW_REQUIRE(staged, "apply_update_stage: null host staging table");
+  return apply_launch(kApplyStage, params, staged, count, blocks_per_tensor, rows, cols, k,
+                      orthogonal, idx, slot, rowd, scale, step, decay, apply_decay, 0.f, stream);
 }
 
 }  // extern "C"

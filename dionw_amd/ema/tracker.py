@@ -9,11 +9,15 @@ step updates every parameter's shadow after the optimizer's own update:
   lerp inside its own pass over the new weights (``fusable_shadows``): a
   parameter it marks as fused skips the queue.
 - CPU shadows: each parameter is copied into its pinned host buffer on a copy
-  stream, the training stream then waits for those copies on the GPU (no host
-  wait), and ``HostEmaWorker`` applies the batch on a background thread. The
-  next due step waits for that batch before reusing the buffers. The optimizer
-  starts the copies of the parameters each of its passes writes right after
-  that pass (``stage_written``), so they overlap the rest of the step.
+  stream, ``HostEmaWorker`` applies the batch on a background thread, and the
+  next step's stream waits for the copies on the GPU before it writes the
+  parameters (no host wait; the caller's forward and backward in between run
+  beside the copies). The next due step waits for the batch before reusing the
+  buffers. The optimizer starts the copies of the parameters each of its
+  passes writes right after that pass (``stage_written``), so they overlap the
+  rest of the step; its matrix apply pass may instead write the snapshots
+  itself, straight from the registers that hold the new weights
+  (``stageable_buffers``, ``mark_staged``; switched by ``fuse_host_copies``).
 
 The reference's tracker (ema/tracker.py:40-299) blocks the host on the
 previous copy at every step instead; the cadence and the arithmetic (lerp with
@@ -109,6 +113,14 @@ class OptimizerIntegratedEMA:
         self._copy_streams: dict[torch.device, torch.cuda.Stream] = {}
         self._fused: set[int] = set()
         self._staged: set[int] = set()
+        self._copies_unjoined = False
+        # Whether the optimizer's matrix apply pass writes CPU EMA snapshots
+        # itself (else they are copied on the copy stream after the pass). The
+        # pass then runs at the host link's rate (~55 GB/s) on the training
+        # stream, while copy-stream copies overlap whatever the caller runs
+        # before the next step (its forward and backward), so it is off unless a
+        # caller whose steps follow each other directly turns it on.
+        self.fuse_host_copies = False
 
     # -- schedule --------------------------------------------------------------
     @property
@@ -129,6 +141,12 @@ class OptimizerIntegratedEMA:
 
     def begin_step(self) -> None:
         """Advance the schedule as an optimizer step starts."""
+        if self._copies_unjoined:
+            # The last due step's snapshot copies read the parameters this step
+            # is about to write.
+            for device, stream in self._copy_streams.items():
+                torch.cuda.current_stream(device).wait_stream(stream)
+            self._copies_unjoined = False
         self._fused.clear()
         self._staged.clear()
         self._count += 1
@@ -189,6 +207,39 @@ class OptimizerIntegratedEMA:
             self._staged.add(id(param))
         self._stage(fresh)
 
+    def stageable_buffers(self, params: list[Tensor]) -> list[Tensor] | None:
+        """The pinned host buffers the optimizer's pass over the new weights of
+        ``params`` may write this step's CPU EMA snapshots into (float32,
+        contiguous, laid out like their contiguous float32 CUDA parameters, not
+        staged yet), else None. Parameters without a shadow get one here."""
+        if self._on_gpu or not self._now.update:
+            return None
+        buffers = []
+        for param in params:
+            entry = self.optimizer.state.get(param)
+            if (entry is None or id(param) in self._staged or not param.is_cuda
+                    or param.dtype is not FP32 or not param.is_contiguous()):
+                return None
+            if EMA_SHADOW not in entry:
+                self._place(param, entry, None, False)
+            staged = entry[EMA_TMP_CPU]
+            if (staged.dtype is not FP32 or staged.shape != param.shape
+                    or not staged.is_contiguous() or not staged.is_pinned()):
+                return None
+            buffers.append(staged)
+        return buffers
+
+    def mark_staged(self, params: list[Tensor]) -> None:
+        """Record that the work just enqueued on the current stream writes the
+        snapshots of ``params`` into their host buffers (``stageable_buffers``)."""
+        if not params:
+            return
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(params[0].device))
+        for param in params:
+            self._snapshot(self.optimizer.state[param], ready)
+            self._staged.add(id(param))
+
     # -- shadows -----------------------------------------------------------------
     def _place(self, param: Tensor, entry: dict[str, Any], shadow: Tensor | None,
                initialized: bool) -> None:
@@ -248,8 +299,6 @@ class OptimizerIntegratedEMA:
         parameters); one event per copy tells the worker when it has landed."""
         joined: set[torch.device] = set()
         for param, entry in items:
-            if self._now.from_live:
-                entry[EMA_INITIALIZED] = False
             staged = entry[EMA_TMP_CPU]
             ready = None
             if param.is_cuda and staged.is_pinned():
@@ -265,9 +314,16 @@ class OptimizerIntegratedEMA:
                     ready.record(stream)
             else:
                 staged.copy_(param)
-            entry[EMA_EVENT] = ready
-            entry[EMA_PENDING] = True
-            self._batch.append(HostSnapshot(entry, ready, entry[EMA_SHADOW], staged))
+            self._snapshot(entry, ready)
+
+    def _snapshot(self, entry: dict[str, Any], ready: torch.cuda.Event | None) -> None:
+        """Queue a parameter whose host buffer is being filled (``ready`` marks
+        the end of the fill) for the host worker."""
+        if self._now.from_live:
+            entry[EMA_INITIALIZED] = False
+        entry[EMA_EVENT] = ready
+        entry[EMA_PENDING] = True
+        self._batch.append(HostSnapshot(entry, ready, entry[EMA_SHADOW], entry[EMA_TMP_CPU]))
 
     @torch.no_grad()
     def _run_device_queues(self) -> None:
@@ -292,9 +348,10 @@ class OptimizerIntegratedEMA:
             self._staged.clear()
             if not batch:
                 return
-            # Later writes of the parameters wait for the copies on the GPU.
-            for device, stream in self._copy_streams.items():
-                torch.cuda.current_stream(device).wait_stream(stream)
+            # The copies may run on beside whatever the caller enqueues until the
+            # next step, which writes the parameters: that step's stream waits for
+            # them first (begin_step), on the GPU.
+            self._copies_unjoined = bool(self._copy_streams)
             self._host.submit(batch, self._lerp_decay())
 
     def flush_pending_updates(self) -> None:

@@ -269,6 +269,22 @@ int dionw_apply_update_ema(float* const* params, float* const* shadows, int32_t 
                            const float* rowd, const float* scale, float step, float decay,
                            int32_t apply_decay, float ema_weight, dionw_stream_t stream);
 
+/*
+ * dionw_apply_update that also writes every row's new weights (also the rows
+ * only decayed or unchanged) into staged[i], a pinned host buffer laid out like
+ * params[i] (hipHostMalloc or torch pin_memory=True; other memory is rejected
+ * before any launch): the CPU EMA's snapshot of the parameters taken by the pass
+ * that forms them. Replaces the apply pass followed by the side-stream
+ * tmp_cpu.copy_(param, non_blocking=True) of every parameter
+ * (_matrix_step.py:274-311, then ema/tracker.py:229-248). The snapshot is
+ * complete once the work enqueued on `stream` up to this call has finished.
+ */
+int dionw_apply_update_stage(float* const* params, float* const* staged, int32_t count,
+                             int64_t blocks_per_tensor, int64_t rows, int64_t cols, int64_t k,
+                             const void* orthogonal, const int32_t* idx, const int32_t* slot,
+                             const float* rowd, const float* scale, float step, float decay,
+                             int32_t apply_decay, dionw_stream_t stream);
+
 /* steps[i] += 1 (float32 device scalars): the _foreach_add_ of _adamw.py:47. */
 int dionw_increment_steps(float* const* steps, int32_t count, dionw_stream_t stream);
 

@@ -332,3 +332,105 @@ def test_cpu_ema_copies_started_after_each_pass_equal_end_of_step_copies(
     for a, b in zip(early_shadows, late_shadows):
         assert a.device.type == "cpu" and torch.equal(a, b)
     assert not torch.equal(early_shadows[0], early_weights[0])  # a real lerp, not a copy
+
+
+@pytest.mark.parametrize(("weight_decay", "fraction", "start"),
+                         [(0.1, 0.5, 0), (0.0, 0.5, 0), (0.0, 1.0, 0), (0.1, 0.25, 3)])
+def test_cpu_ema_snapshots_written_by_the_apply_pass_equal_copied_ones(
+        weight_decay: float, fraction: float, start: int,
+        monkeypatch: pytest.MonkeyPatch) -> None:
+    """CPU EMA: the matrix apply pass writes each parameter's host snapshot
+    itself (every row, also rows neither selected nor decayed), and the shadows
+    equal those of snapshots copied on the copy stream, bit for bit, through a
+    restart from the live weights (start_step) and lerps."""
+    from dionw_amd import _lib
+
+    original = _lib.call
+
+    def run(fuse: bool):
+        names: list[str] = []
+
+        def recording(name, *args):
+            names.append(name)
+            return original(name, *args)
+
+        monkeypatch.setattr(_lib, "call", recording)
+        g = torch.Generator().manual_seed(9)
+        weights = [nn.Parameter(torch.randn(128, 96, generator=g).cuda()),
+                   nn.Parameter(torch.randn(128, 96, generator=g).cuda()),
+                   nn.Parameter(torch.randn(96, 130, generator=g).cuda()),
+                   nn.Parameter(torch.randn(96, generator=g).cuda())]
+        opt = dionw.Dion(
+            [{"params": weights[:3], dionw.ROUTE_KEY: "matrix", dionw.FRACTION_KEY: fraction},
+             {"params": weights[3:], dionw.ROUTE_KEY: "adamw"}],
+            lr=1e-2, weight_decay=weight_decay, ema=_config(EMADevice.CPU, 0.9, start=start))
+        opt.ema.fuse_host_copies = fuse
+        for _ in range(6):
+            for w in weights:
+                w.grad = torch.randn(w.shape, generator=g).cuda()
+            opt.step()
+        opt.ema.flush_pending_updates()
+        monkeypatch.setattr(_lib, "call", original)
+        return ([_shadow(opt, w).clone() for w in weights], [w.detach().cpu() for w in weights],
+                names)
+
+    fused_shadows, fused_weights, fused_names = run(True)
+    copied_shadows, copied_weights, copied_names = run(False)
+    assert "dionw_apply_update_stage" in fused_names
+    assert "dionw_apply_update_stage" not in copied_names
+    for a, b in zip(fused_weights, copied_weights):
+        assert torch.equal(a, b)
+    for a, b in zip(fused_shadows, copied_shadows):
+        assert a.device.type == "cpu" and torch.equal(a, b)
+    assert not torch.equal(fused_shadows[0], fused_weights[0])  # a real lerp, not a copy
+
+
+def test_apply_stage_writes_every_row_to_pinned_host_memory() -> None:
+    """dionw_apply_update_stage through the C ABI: with row selection and no
+    weight decay, the host buffers receive every row of the new weights (the
+    unselected rows unchanged), and the device update equals dionw_apply_update's."""
+    from dionw_amd import _lib
+
+    g = torch.Generator().manual_seed(3)
+    blocks_per, rows, cols, k, count = 2, 64, 72, 16, 3
+    start = [torch.randn(blocks_per * rows, cols, generator=g) for _ in range(count)]
+    orth = (torch.randn(count * blocks_per, k, cols, generator=g) * 0.1).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(rows, generator=g)[:k].sort().values
+                       for _ in range(count * blocks_per)]).to(torch.int32)
+    slot = torch.full((count * blocks_per, rows), -1, dtype=torch.int32)
+    for b in range(count * blocks_per):
+        slot[b, idx[b].long()] = torch.arange(k, dtype=torch.int32)
+    dev = [t.cuda() for t in (orth, idx, slot)]
+    plain = [t.clone().cuda() for t in start]
+    staged_w = [t.clone().cuda() for t in start]
+    host = [torch.full_like(t, float("nan")).pin_memory() for t in start]
+    common = (count, blocks_per, rows, cols, k, dev[0].data_ptr(), dev[1].data_ptr(),
+              dev[2].data_ptr(), None, None, 0.5, 1.0, 0)
+    stream = _lib.stream_handle()
+    _lib.call("dionw_apply_update", _lib.ptr_array(plain), *common, stream)
+    _lib.call("dionw_apply_update_stage", _lib.ptr_array(staged_w), _lib.ptr_array(host),
+              *common, stream)
+    torch.cuda.synchronize()
+    for p, s, h, w0 in zip(plain, staged_w, host, start):
+        assert torch.equal(p, s)
+        assert torch.equal(h, s.cpu())
+        assert not torch.equal(h, w0)
+
+
+def test_apply_stage_rejects_memory_that_is_not_pinned_host_memory() -> None:
+    """Device memory or pageable host memory as a staging buffer is refused on
+    the host, before any launch, and leaves no HIP error behind."""
+    from dionw_amd import _lib
+
+    w = [torch.zeros(8, 16, device="cuda")]
+    orth = torch.zeros(1, 8, 16, dtype=torch.bfloat16, device="cuda")
+    common = (1, 1, 8, 16, 8, orth.data_ptr(), None, None, None, None, 0.5, 1.0, 0)
+    stream = _lib.stream_handle()
+    for bad in (torch.zeros(8, 16, device="cuda"), torch.zeros(8, 16)):
+        with pytest.raises(ValueError, match="pinned host memory"):
+            _lib.call("dionw_apply_update_stage", _lib.ptr_array(w), _lib.ptr_array([bad]),
+                      *common, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(w[0], torch.zeros_like(w[0]))
+    torch.zeros(4, device="cuda").add_(1)  # the runtime is still usable
+    torch.cuda.synchronize()
