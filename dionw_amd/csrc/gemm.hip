@@ -1040,7 +1040,6 @@ int64_t wgs_of(const Problem& p, int tile) {
 // there).
 // Both in twentieths of a 256x256 round (a 128x128 round is 0.65).
 constexpr int kBigRound = 20, kMidRound = 13;
-constexpr double kMidRate = (double)kMidRound / kBigRound;
 int64_t big_cost(const Problem& p) { return kBigRound * ((wgs_of(p, 256) + 255) / 256); }
 int64_t mid_cost(const Problem& p) { return kMidRound * ((wgs_of(p, 128) + 511) / 512); }
 
@@ -1126,8 +1125,9 @@ int launch(const Problem& p, hipStream_t stream) {
 // Time in 256x256 rounds times k (a round of 256x256 tiles over depth k costs
 // k, a round of two 128x128 tiles per CU kGroupMidRate k: the rate the grouping
 // choices were measured with, e.g. gram-ns's lone-run pair on 128x128 tiles,
-// 1.35 -> 1.32 ms; the launcher's own tile rule counts kMidRate). Alone, each product takes its
-// better tile (the launcher's rule); grouped, the tiles of all of them fill the
+// 1.35 -> 1.32 ms; the launcher's own tile rule counts kMidRound / kBigRound).
+// Alone, each product takes its better tile (the launcher's rule); grouped, the
+// tiles of all of them fill the
 // CUs longest first, which costs their total work over the CUs plus about half
 // a round of the shortest tiles, and no less than the longest tile.
 //
