@@ -215,87 +215,67 @@ __global__ __launch_bounds__(256) void prepare_kernel(PrepArgs a) {
   const int64_t p_base = (int64_t)blockIdx.y * kTile;
   const float den = a.den[b];
 
-  // A lane's four rows: every load is issued before the first store (a store to
-  // M may alias a later row's load, so the compiler would not hoist them).
-  float* mrow[4];
-  const IN* grow[4];
-  bool live[4];
+  T vals[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t p = p_base + ty + 16 * i;
-    live[i] = p < a.k;
-    mrow[i] = nullptr;
-    grow[i] = nullptr;
-    if (live[i]) {
+    float u[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p < a.k) {
       const int64_t src_row = a.full ? p : (int64_t)a.idx[b * a.k + p];
-      mrow[i] = a.momentum ? a.momentum + (b * a.rows + src_row) * a.cols : nullptr;
+      float* m = a.momentum ? a.momentum + (b * a.rows + src_row) * a.cols : nullptr;
+      const IN* g = nullptr;
       if (a.full) {
         const int64_t tensor = b / a.blocks_per_tensor;
         const int64_t local_row = (b - tensor * a.blocks_per_tensor) * a.rows + p;
-        grow[i] = reinterpret_cast<const IN*>(a.t.grad[tensor]) + local_row * a.cols;
+        g = reinterpret_cast<const IN*>(a.t.grad[tensor]) + local_row * a.cols;
       }
-    }
-  }
-  const bool vec4 = a.vec && j0 + 3 < a.cols;
-  float u[4][4];
-  if (vec4) {
-    f32x4 mv[4], gv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      mv[i] = live[i] && mrow[i] ? *reinterpret_cast<const f32x4*>(mrow[i] + j0)
-                                 : f32x4{0.f, 0.f, 0.f, 0.f};
-      gv[i] = live[i] && a.full ? load4_nt(grow[i] + j0, 0) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 uv, nm;
-      if (a.full) {
-        const f32x4 sum = mv[i] + gv[i];
-        nm = sum * a.mu;
-        uv = a.nesterov ? gv[i] + nm : sum;
-      } else {
-        uv = mv[i];
-        nm = mv[i] * a.mu;
-      }
-      if (live[i] && a.write_m) *reinterpret_cast<f32x4*>(mrow[i] + j0) = nm;
-      u[i][0] = uv.x; u[i][1] = uv.y; u[i][2] = uv.z; u[i][3] = uv.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int64_t j = j0 + c;
-        u[i][c] = 0.f;
-        if (!live[i] || j >= a.cols) continue;
-        float mv = mrow[i] ? mrow[i][j] : 0.f, uv, nm;
+      if (a.vec && j0 + 3 < a.cols) {
+        f32x4 mv = m ? *reinterpret_cast<const f32x4*>(m + j0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 uv, nm;
         if (a.full) {
-          float gv = (float)grow[i][j];
-          float sum = mv + gv;
-          nm = sum * a.mu;
-          uv = a.nesterov ? gv + nm : sum;
+          f32x4 gv = load4_nt(g + j0, 0);
+          f32x4 s = mv + gv;
+          nm = s * a.mu;
+          uv = a.nesterov ? gv + nm : s;
         } else {
           uv = mv;
           nm = mv * a.mu;
         }
-        if (a.write_m) mrow[i][j] = nm;
-        u[i][c] = uv;
-      }
-  }
-  T vals[4][4];
+        if (a.write_m) *reinterpret_cast<f32x4*>(m + j0) = nm;
+        u[0] = uv.x; u[1] = uv.y; u[2] = uv.z; u[3] = uv.w;
+      } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+        for (int c = 0; c < 4; ++c) {
+          const int64_t j = j0 + c;
+          if (j < a.cols) {
+            float mv = m ? m[j] : 0.f, uv, nm;
+            if (a.full) {
+              float gv = (float)g[j];
+              float s = mv + gv;
+              nm = s * a.mu;
+              uv = a.nesterov ? gv + nm : s;
+            } else {
+              uv = mv;
+              nm = mv * a.mu;
+            }
+            if (a.write_m) m[j] = nm;
+            u[c] = uv;
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float x;
       if (ELEM == kBF16) {
         // Keller / Polar Express: the input is rounded to bf16 before the division.
-        x = (float)(__bf16)u[i][c] / den;
+        x = (float)(__bf16)u[c] / den;
       } else {
-        x = u[i][c] / den;
+        x = u[c] / den;
       }
       vals[i][c] = (T)x;  // padding rows/cols hold u = 0 -> 0
     }
+  }
   // Row-major output [P_pad, J_pad] (may be skipped).
   T* out_r = a.out_r ? reinterpret_cast<T*>(a.out_r) + b * a.p_pad * a.j_pad : nullptr;
 #pragma unroll
