@@ -403,7 +403,11 @@ def test_apply_stage_writes_every_row_to_pinned_host_memory() -> None:
     dev = [t.cuda() for t in (orth, idx, slot)]
     plain = [t.clone().cuda() for t in start]
     staged_w = [t.clone().cuda() for t in start]
-    host = [torch.full_like(t, float("nan")).pin_memory() for t in start]
+    # The last buffer is a view that starts inside a larger pinned allocation:
+    # the device address the library looks up must keep its offset.
+    host = [torch.full_like(t, float("nan")).pin_memory() for t in start[:-1]]
+    pool = torch.full((2 * start[-1].numel() + 4,), float("nan")).pin_memory()
+    host.append(pool[start[-1].numel() + 4:].view(start[-1].shape))
     common = (count, blocks_per, rows, cols, k, dev[0].data_ptr(), dev[1].data_ptr(),
               dev[2].data_ptr(), None, None, 0.5, 1.0, 0)
     stream = _lib.stream_handle()
@@ -415,6 +419,7 @@ def test_apply_stage_writes_every_row_to_pinned_host_memory() -> None:
         assert torch.equal(p, s)
         assert torch.equal(h, s.cpu())
         assert not torch.equal(h, w0)
+    assert bool(pool[: start[-1].numel() + 4].isnan().all())  # nothing written before the view
 
 
 def test_apply_stage_rejects_memory_that_is_not_pinned_host_memory() -> None:
