@@ -30,6 +30,9 @@ from dionw_amd.optimizer import Dion
 from dionw_amd.param_groups import ParamGroups, param_groups
 from dionw_amd.report import RoutedParameter, RouteReason, RoutingReport
 from dionw_amd.routing import Route, RouteKind, RouteProvider
+# Not in the reference: frees the device scratch the HIP passes keep between steps
+# (it grows to the largest run queued; a later step allocates it again).
+from dionw_amd._workspace import release as release_workspace  # noqa: F401
 
 __version__ = "0.1.0"
 
