@@ -176,5 +176,6 @@ def test_workspace_is_keyed_by_device_and_stream() -> None:
     assert _workspace.buffer(cpu, "t", (2,), torch.float32, stream=1).data_ptr() == a.data_ptr()
     grown = _workspace.buffer(cpu, "t", (1000,), torch.float32, stream=1)
     assert grown.numel() == 1000 and _workspace.held_bytes(cpu) >= 4000
-    _workspace.release(cpu)
+    import dionw_amd
+    dionw_amd.release_workspace(cpu)  # the public name of the same release
     assert _workspace.held_bytes(cpu) == 0
