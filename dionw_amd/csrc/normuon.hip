@@ -339,7 +339,10 @@ int stats_launch(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows
                  float* partials, float* scale, hipStream_t stream) {
   DIONW_REQUIRE(orthogonal && variance && rowd && partials && scale,
                 "normuon_stats: null pointer");
-  DIONW_REQUIRE(k > 0 && k <= rows && cols > 0, "normuon_stats: bad sizes");
+  DIONW_REQUIRE(blocks >= 0 && k > 0 && k <= rows && cols > 0, "normuon_stats: bad sizes");
+  DIONW_REQUIRE(blocks < (int64_t{1} << 31) && ceil_div(blocks * k, 4) <= INT32_MAX,
+                "normuon_stats: %lld blocks x %lld selected rows exceed one launch",
+                (long long)blocks, (long long)k);
   DIONW_REQUIRE(idx || k == rows, "normuon_stats: every-row mode needs k == rows");
   if (blocks == 0) return kOk;
   StatArgs a{};
@@ -421,7 +424,8 @@ int dionw_normuon_stats(const void* orthogonal, int64_t blocks, int64_t k, int64
 int dionw_normuon_stats_noalloc(const void* orthogonal, int64_t blocks, int64_t k, int64_t rows,
                                 int64_t cols, const int32_t* idx, float* variance, float beta2,
                                 float step, float* rowd, float* scale, hipStream_t stream) {
-  DIONW_REQUIRE(blocks <= 0 || k <= 0 || (k <= kNoAllocRows && blocks <= kNoAllocRows / k),
+  DIONW_REQUIRE(blocks >= 0, "normuon_stats: bad sizes");
+  DIONW_REQUIRE(blocks == 0 || k <= 0 || (k <= kNoAllocRows && blocks <= kNoAllocRows / k),
                 "normuon_stats_noalloc: %lld blocks x %lld selected rows exceed the %lld rows "
                 "of its device scratch (use dionw_normuon_stats with a caller workspace)",
                 (long long)blocks, (long long)k, (long long)kNoAllocRows);

@@ -69,10 +69,15 @@ def padded_sides(rows: int, cols: int) -> tuple[int, int]:
     prepared input: both sides rounded up to 8; a short side that is then an odd
     multiple of 32 (at least 256) grows by 32 more, so that the products whose
     depth is that side run 64-deep LDS stages (the padding rows are zero, which
-    every polynomial here keeps exactly zero, and are never stored)."""
+    every polynomial here keeps exactly zero, and are never stored).
+
+    The short side grows only while it stays no longer than the long side: the
+    iteration runs in the orientation of the unpadded block (wide: short side
+    first), and the library needs the first padded extent to be the shorter.
+    """
     p_pad, j_pad = _round8(rows), _round8(cols)
-    short = min(p_pad, j_pad)
-    if PAD_SHORT_SIDE_TO_64 and short >= 256 and short % 64 == 32:
+    short, long = min(p_pad, j_pad), max(p_pad, j_pad)
+    if PAD_SHORT_SIDE_TO_64 and short >= 256 and short % 64 == 32 and short + 32 <= long:
         if rows <= cols:
             p_pad += 32
         else:

@@ -9,10 +9,16 @@ quintics) it runs on sampled blocks: blocks never interact, so a sample is
 checked exactly as the whole would be.
 
 Bars (the north star's, with the build's update-level bar): row selection and
-momentum bit-exact; the update ``W_new - W d`` within 1e-2 relative Frobenius
-of the oracle's for the float16 Gram iteration (3e-2 for the bfloat16
-quintic); parameters within 2e-3; AdamW and the EMA bit-exact against torch's
-own fused AdamW and ``_foreach_lerp_``.
+momentum bit-exact; the update ``W_new - W d`` within ``1.6 e + 3e-3``
+relative Frobenius of the oracle's, where ``e`` is the oracle's own
+Newton-Schulz rounding error on the same input (its distance to the same
+polynomials in float64); parameters within 2e-3; AdamW and the EMA bit-exact
+against torch's own fused AdamW and ``_foreach_lerp_``. The configurations run
+their full step counts (configs 3 and 5: 10 steps; config 4: 5 steps over all
+32 layers): every block's momentum is checked at every step on the GPU (every
+row is either ``M + G`` or ``fp32((M + G) mu)``, exactly ``k`` decayed rows per
+block), and two sampled blocks per bucket against the oracle, from the GPU's
+state before the step.
 """
 
 from __future__ import annotations
@@ -79,6 +85,94 @@ def _check_run(name: str, params: list[nn.Parameter], opt: Dion, before: torch.T
     assert rel_fro(got_w, w_ref) < 2e-3, f"{name}: parameters"
     got_v = torch.stack([opt.state[p]["variance"].cpu() for p in params]).view(var_ref.shape)
     assert rel_fro(got_v, var_ref) < 2e-2, f"{name}: NorMuon variance"
+
+
+POLYNOMIALS = {"gram": (dion_ref.GRAM_COEFFICIENTS, 1.0),
+               "keller_triton": (dion_ref.KELLER_COEFFICIENTS, dion_ref.KELLER_NORM_SAFETY)}
+
+
+def _recording_oracle(kind: str, seen: dict):
+    """The oracle's orthogonalization of ``kind``, recording its rounding error
+    (distance to the same polynomials in float64) in ``seen["rounding"]``."""
+    def ortho(x: torch.Tensor, epsilon: float) -> torch.Tensor:
+        out = dion_ref.ORTHOGONALIZE[kind](x, epsilon)
+        tall = x.shape[-2] > x.shape[-1]
+        target = dion_ref.polynomial_float64(x.mT if tall else x, *POLYNOMIALS[kind])
+        seen["rounding"] = max(seen.get("rounding", 0.0),
+                               rel_fro(out.float(), target.mT if tall else target))
+        return out
+    return ortho
+
+
+def _momentum_of(opt: Dion, p: nn.Parameter) -> torch.Tensor:
+    """A parameter's momentum before its first step is zero."""
+    m = opt.state[p].get("momentum")
+    return torch.zeros_like(p) if m is None else m.detach().clone()
+
+
+def _check_every_block(name: str, params: list[nn.Parameter], opt: Dion,
+                       m_old: list[torch.Tensor], k: int) -> None:
+    """Every block's momentum on the GPU: ``s = M + G`` (one exact float32
+    add); a selected row is ``fp32(s mu)``, every other row ``s``, and each
+    block decays exactly ``k`` rows (a row equal both ways, all zero, counts
+    either way)."""
+    mu = torch.tensor(MU, dtype=torch.float32, device=DEV)
+    for i, (p, m0) in enumerate(zip(params, m_old)):
+        m_new = opt.state[p]["momentum"]
+        total = m0 + p.grad
+        is_decayed = (m_new == total * mu).all(-1)
+        is_kept = (m_new == total).all(-1)
+        assert bool((is_decayed | is_kept).all()), f"{name} block {i}: a row is neither"
+        only_decayed = int((is_decayed & ~is_kept).sum())
+        either = int((is_decayed & is_kept).sum())
+        assert only_decayed <= k <= only_decayed + either, (
+            f"{name} block {i}: {only_decayed} decayed rows, expected {k}")
+
+
+def _check_sampled(name: str, params: list[nn.Parameter], opt: Dion, sample: list[int],
+                   before: dict, k: int, kind: str = "gram", normuon: bool = True,
+                   nesterov: bool = False) -> None:
+    """The sampled blocks' step against the oracle, from the GPU's state
+    ``before`` the step (weights, momentum, variance, gradient of each)."""
+    w = torch.stack([before[i][0] for i in sample])
+    mom = torch.stack([before[i][1] for i in sample])
+    var = torch.stack([before[i][2] for i in sample])
+    grad = torch.stack([before[i][3] for i in sample])
+    start = w.clone()
+    seen: dict = {}
+    dion_ref.step_blocks(w, grad, mom, var, k=k, lr=LR, mu=MU, beta2=BETA2, weight_decay=WD,
+                         kind=kind, normuon=normuon, nesterov=nesterov,
+                         orthogonalize=_recording_oracle(kind, seen))
+    got_m = torch.stack([opt.state[params[i]]["momentum"].cpu() for i in sample])
+    assert torch.equal(got_m, mom), f"{name}: momentum of blocks {sample} differs"
+    got_w = torch.stack([params[i].detach().cpu() for i in sample])
+    decay = 1.0 - LR * WD
+    err = rel_fro(got_w - start * decay, w - start * decay)
+    bar = 1.6 * seen["rounding"] + 3e-3
+    assert err < bar, f"{name}: update rel err {err}, bar {bar} (blocks {sample})"
+    assert rel_fro(got_w, w) < 2e-3, f"{name}: parameters of blocks {sample}"
+    if normuon:
+        got_v = torch.stack([opt.state[params[i]]["variance"].cpu() for i in sample])
+        assert rel_fro(got_v, var) < 2e-2, f"{name}: NorMuon variance of blocks {sample}"
+
+
+def _state_before(opt: Dion, params: list[nn.Parameter], sample: list[int]) -> dict:
+    """(weights, momentum, variance, gradient) of the sampled blocks, on the host."""
+    out = {}
+    for i in sample:
+        p = params[i]
+        var = opt.state[p].get("variance")
+        var = torch.zeros(p.shape[0], 1) if var is None else var.detach().cpu().clone()
+        out[i] = (p.detach().cpu().clone(), _momentum_of(opt, p).cpu(), var.view(-1, 1),
+                  p.grad.detach().cpu().clone())
+    return out
+
+
+def _sample(n: int, step: int) -> list[int]:
+    """Two distinct blocks of ``n`` that move with the step."""
+    a = (7 * step) % n
+    b = (n - 1 - 3 * step) % n
+    return [a, b] if a != b else [a, (a + 1) % n]
 
 
 # ---- products at the tile counts that switch on XCD run dealing ---------------
@@ -178,6 +272,61 @@ def test_config4_llama_layer_step() -> None:
                        mom, var, 1e-2)
 
 
+def test_config4_llama3_8b_full_steps() -> None:
+    """The whole Llama-3-8B step bench.py times (``bench.build_llama``: 32
+    layers, Dion f = 0.25 on every linear, AdamW on the two 128256 x 4096
+    embeddings with weight decay and on the 65 RMSNorm weights without), five
+    steps with new gradients each. At every step: AdamW bit for bit against
+    torch.optim.AdamW(fused=True) on twins of the same tensors (1.05 G
+    elements, the embeddings' 128 k chunks per tensor included); every block's
+    momentum and selection count; two sampled blocks per bucket against the
+    oracle from the GPU's state before the step."""
+    import bench
+
+    _say("config 4: Llama-3-8B, all 32 layers, 5 steps")
+    dev = torch.device(DEV)
+    groups, n_params = bench.build_llama(torch, dev, bench.LLAMA, 0.25)
+    assert n_params == 8_030_261_248
+    embeds, norms, matrices = (grp["params"] for grp in groups)
+    opt = Dion(groups, lr=LR, weight_decay=WD, momentum=MU, muon_beta2=BETA2,
+               betas=(0.9, 0.95), eps=1e-8)
+    twins = [nn.Parameter(p.detach().clone()) for p in embeds + norms]
+    torch_opt = torch.optim.AdamW(
+        [{"params": twins[:2]}, {"params": twins[2:], "weight_decay": 0.0}],
+        lr=LR, betas=(0.9, 0.95), weight_decay=WD, eps=1e-8, fused=True)
+    per_layer = len(LLAMA_LAYER)
+    by_name = {name: matrices[i::per_layer] for i, (name, _, _) in enumerate(LLAMA_LAYER)}
+    buckets = {"q/o": [p for pair in zip(by_name["q"], by_name["o"]) for p in pair],
+               "k/v": [p for pair in zip(by_name["k"], by_name["v"]) for p in pair],
+               "gate/up": [p for pair in zip(by_name["gate"], by_name["up"]) for p in pair],
+               "down": by_name["down"]}
+    g = torch.Generator(device=DEV).manual_seed(4)
+    try:
+        for step in range(5):
+            for p in matrices + embeds + norms:
+                p.grad.normal_(0.0, 1e-3, generator=g)
+            for p, t in zip(embeds + norms, twins):
+                t.grad = p.grad.clone()
+            samples = {b: _sample(len(ps), step) for b, ps in buckets.items()}
+            before = {b: _state_before(opt, ps, samples[b]) for b, ps in buckets.items()}
+            m_old = {b: [_momentum_of(opt, p) for p in ps] for b, ps in buckets.items()}
+            opt.step()
+            torch_opt.step()
+            torch.cuda.synchronize()
+            _say(f"config 4: step {step} done, checking")
+            for p, t in zip(embeds + norms, twins):
+                assert torch.equal(p.detach(), t.detach()), f"step {step}: AdamW {tuple(p.shape)}"
+            for bname, ps in buckets.items():
+                k = math.ceil(0.25 * ps[0].shape[0])
+                _check_every_block(f"step {step} {bname}", ps, opt, m_old[bname], k)
+                _check_sampled(f"step {step} {bname}", ps, opt, samples[bname], before[bname], k)
+            del m_old
+    finally:
+        del opt, torch_opt, twins, groups, embeds, norms, matrices, by_name, buckets
+        _workspace.release()
+        torch.cuda.empty_cache()
+
+
 def test_config4_grouped_newton_schulz_at_bucket_shapes() -> None:
     """The Newton-Schulz call of a whole Llama-3-8B step: the four runs at their
     32-layer bucket sizes in one grouped call (the 24 launches bench.py times,
@@ -232,9 +381,10 @@ GPT2_MATRICES = [("qkv", 2304, 768), ("proj", 768, 768), ("fc", 3072, 768), ("fc
 def test_config3_gpt2_small_step() -> None:
     """GPT-2 small (124 M parameters): 12 layers of qkv, proj, fc, fc2 on Dion
     with every row updated (768-wide sides), AdamW on wte 50257 x 768, wpe,
-    LayerNorms and biases. Two steps; Dion buckets against the oracle, AdamW
-    bit for bit against torch.optim.AdamW(fused=True)."""
-    _say("config 3: GPT-2 small, 2 steps")
+    LayerNorms and biases. Ten steps: every block's momentum, two sampled
+    blocks per bucket against the oracle, AdamW bit for bit against
+    torch.optim.AdamW(fused=True) at every step."""
+    _say("config 3: GPT-2 small, 10 steps")
     g = torch.Generator(device=DEV).manual_seed(0)
     mats = {name: [nn.Parameter(_normal(g, rows, cols, std=0.02)) for _ in range(12)]
             for name, rows, cols in GPT2_MATRICES}
@@ -251,30 +401,25 @@ def test_config3_gpt2_small_step() -> None:
     torch_opt = torch.optim.AdamW(
         [{"params": twins[:2]}, {"params": twins[2:], "weight_decay": 0.0}],
         lr=LR, betas=(0.9, 0.95), weight_decay=WD, eps=1e-8, fused=True)
-    ref = {name: (torch.stack([p.detach().cpu() for p in ps]),
-                  torch.zeros(12, ps[0].shape[0], ps[0].shape[1]),
-                  torch.zeros(12, ps[0].shape[0], 1)) for name, ps in mats.items()}
-    for step in range(2):
-        grads = {name: [_normal(g, *p.shape, std=1e-3) for p in ps] for name, ps in mats.items()}
-        for name, ps in mats.items():
-            for p, gr in zip(ps, grads[name]):
-                p.grad = gr
+    for step in range(10):
+        for ps in mats.values():
+            for p in ps:
+                p.grad = _normal(g, *p.shape, std=1e-3)
         for p, t in zip(embeds + vectors, twins):
             p.grad = _normal(g, *p.shape, std=1e-3)
             t.grad = p.grad.clone()
-        before = {name: torch.stack([p.detach().cpu() for p in ps]) for name, ps in mats.items()}
+        sample = _sample(12, step)
+        before = {name: _state_before(opt, ps, sample) for name, ps in mats.items()}
+        m_old = {name: [_momentum_of(opt, p) for p in ps] for name, ps in mats.items()}
         opt.step()
         torch_opt.step()
         torch.cuda.synchronize()
         for p, t in zip(embeds + vectors, twins):
             assert torch.equal(p.detach(), t.detach()), f"step {step}: AdamW {tuple(p.shape)}"
         for name, ps in mats.items():
-            _, mom, var = ref[name]
-            w = before[name].clone()
-            grad = torch.stack([gr.cpu() for gr in grads[name]])
-            dion_ref.step_blocks(w, grad, mom, var, k=w.shape[1], lr=LR, mu=MU, beta2=BETA2,
-                                 weight_decay=WD, kind="gram")
-            _check_run(f"step {step} {name}", ps, opt, before[name], w, mom, var, 1e-2)
+            _check_every_block(f"step {step} {name}", ps, opt, m_old[name], ps[0].shape[0])
+            _check_sampled(f"step {step} {name}", ps, opt, sample, before[name],
+                           k=ps[0].shape[0])
 
 
 # ---- config 5: MoE expert stack ---------------------------------------------------
@@ -291,10 +436,11 @@ def _experts(g: torch.Generator) -> list[nn.Parameter]:
 def test_config5a_moe_dion_with_gpu_ema() -> None:
     """64 experts (gate/up 1408 x 2048 with k = 352, down 2048 x 1408 with k =
     512), Dion f = 0.25, Student-t(3) gradients, GPU EMA 0.9999 every step
-    (a copy at step 1, then the lerp fused into the apply pass). Two steps;
-    every block against the oracle, the shadows bit for bit against
+    (a copy at step 1, then the lerp fused into the apply pass). Ten steps:
+    every block's momentum and selection count, two sampled blocks per bucket
+    against the oracle, and every shadow bit for bit against
     torch._foreach_lerp_ of the new weights."""
-    _say("config 5a: MoE Dion + GPU EMA, 2 steps")
+    _say("config 5a: MoE Dion + GPU EMA, 10 steps")
     g = torch.Generator(device=DEV).manual_seed(0)
     experts = _experts(g)
     opt = Dion([{"params": experts, ROUTE_KEY: "matrix", FRACTION_KEY: 0.25}], lr=LR,
@@ -302,15 +448,13 @@ def test_config5a_moe_dion_with_gpu_ema() -> None:
                ema=EMAConfig(decay=0.9999, update_every_n_steps=1))
     buckets = {"gate/up": [p for i, p in enumerate(experts) if i % 3 != 2],
                "down": experts[2::3]}
-    ref = {}
-    for bname, ps in buckets.items():
-        w = torch.stack([p.detach().cpu() for p in ps])
-        ref[bname] = (torch.zeros_like(w), torch.zeros(w.shape[0], w.shape[1], 1))
     shadows = None
-    for step in range(2):
+    for step in range(10):
         for p in experts:
             p.grad = _student_t(g, *p.shape)
-        before = {b: torch.stack([p.detach().cpu() for p in ps]) for b, ps in buckets.items()}
+        samples = {b: _sample(len(ps), step) for b, ps in buckets.items()}
+        before = {b: _state_before(opt, ps, samples[b]) for b, ps in buckets.items()}
+        m_old = {b: [_momentum_of(opt, p) for p in ps] for b, ps in buckets.items()}
         opt.step()
         opt.ema.flush_pending_updates()
         torch.cuda.synchronize()
@@ -322,44 +466,32 @@ def test_config5a_moe_dion_with_gpu_ema() -> None:
         for i, (p, s) in enumerate(zip(experts, shadows)):
             assert torch.equal(opt.state[p]["ema_shadow"], s), f"step {step}: shadow {i}"
         for bname, ps in buckets.items():
-            mom, var = ref[bname]
-            w = before[bname].clone()
-            rows = w.shape[1]
-            grad = torch.stack([p.grad.cpu() for p in ps])
-            dion_ref.step_blocks(w, grad, mom, var, k=math.ceil(0.25 * rows), lr=LR, mu=MU,
-                                 beta2=BETA2, weight_decay=WD, kind="gram")
-            _check_run(f"step {step} {bname}", ps, opt, before[bname], w, mom, var, 1e-2)
+            k = math.ceil(0.25 * ps[0].shape[0])
+            _check_every_block(f"step {step} {bname}", ps, opt, m_old[bname], k)
+            _check_sampled(f"step {step} {bname}", ps, opt, samples[bname], before[bname], k)
 
 
 def test_config5b_moe_muon_update() -> None:
     """The same 64 experts with MUON_UPDATE (KELLER_TRITON bfloat16 quintic,
-    Nesterov, every row, no row normalization). Two steps; momentum bit for bit on every
-    expert, experts 0 and 63 (six blocks) against the oracle."""
-    _say("config 5b: MoE MUON_UPDATE, 2 steps")
+    Nesterov, every row, no row normalization). Ten steps: momentum bit for
+    bit on every expert, two sampled blocks per bucket against the oracle."""
+    _say("config 5b: MoE MUON_UPDATE, 10 steps")
     g = torch.Generator(device=DEV).manual_seed(0)
     experts = _experts(g)
     opt = Dion([{"params": experts, ROUTE_KEY: "matrix", FRACTION_KEY: 1.0}], lr=LR,
                momentum=MU, muon_beta2=BETA2, weight_decay=WD, matrix_update=MUON_UPDATE)
-    sample = [0, 1, 2, 189, 190, 191]
-    mom_all = [torch.zeros_like(p) for p in experts]
-    ref_m = {i: torch.zeros(1, *experts[i].shape) for i in sample}
-    for step in range(2):
+    buckets = {"gate/up": [p for i, p in enumerate(experts) if i % 3 != 2],
+               "down": experts[2::3]}
+    for step in range(10):
         for p in experts:
             p.grad = _student_t(g, *p.shape)
-        before = {i: experts[i].detach().cpu()[None] for i in sample}
+        samples = {b: _sample(len(ps), step) for b, ps in buckets.items()}
+        before = {b: _state_before(opt, ps, samples[b]) for b, ps in buckets.items()}
+        m_old = {b: [_momentum_of(opt, p) for p in ps] for b, ps in buckets.items()}
         opt.step()
         torch.cuda.synchronize()
-        for i, (p, m) in enumerate(zip(experts, mom_all)):
-            m.add_(p.grad).mul_(MU)
-            assert torch.equal(opt.state[p]["momentum"], m), f"step {step}: momentum {i}"
-        decay = 1.0 - LR * WD
-        for i in sample:
-            w = before[i].clone()
-            var = torch.zeros(1, w.shape[1], 1)
-            dion_ref.step_blocks(w, experts[i].grad.cpu()[None], ref_m[i], var, k=w.shape[1],
-                                 lr=LR, mu=MU, beta2=BETA2, weight_decay=WD,
-                                 kind="keller_triton", normuon=False, nesterov=True)
-            got = experts[i].detach().cpu()[None]
-            err = rel_fro(got - before[i] * decay, w - before[i] * decay)
-            assert err < 3e-2, f"step {step} expert block {i}: update rel err {err}"
-            assert rel_fro(got, w) < 2e-3, f"step {step} expert block {i}: parameters"
+        for bname, ps in buckets.items():
+            rows = ps[0].shape[0]
+            _check_every_block(f"step {step} {bname}", ps, opt, m_old[bname], rows)
+            _check_sampled(f"step {step} {bname}", ps, opt, samples[bname], before[bname],
+                           rows, kind="keller_triton", normuon=False, nesterov=True)

@@ -131,6 +131,21 @@ def test_grouped_newton_schulz_rejects_overlapping_workspaces() -> None:
                   arr(ctypes.c_size_t, 0, 0), None)
 
 
+def test_normuon_stats_rejects_negative_block_counts() -> None:
+    """A negative block count is rejected by both NorMuon statistics entry
+    points before any launch or device lookup (the fake addresses are never
+    dereferenced; a wrapped count would otherwise size a huge grid)."""
+    fake = 1 << 40
+    args = (fake, -1, 4, 8, 16, fake, fake, 0.95, -0.01, fake)
+    with pytest.raises(ValueError, match="bad sizes"):
+        _lib.call("dionw_normuon_stats", *args, fake, fake, None)
+    with pytest.raises(ValueError, match="bad sizes"):
+        _lib.call("dionw_normuon_stats_noalloc", *args, fake, None)
+    with pytest.raises(ValueError, match="exceed one launch"):
+        _lib.call("dionw_normuon_stats", fake, 1 << 31, 4, 8, 16, fake, fake, 0.95, -0.01, fake,
+                  fake, fake, None)
+
+
 def test_prepared_orientations() -> None:
     """The iterate is the wide orientation; its transpose is prepared only when
     the short side, rounded up to 8, is not a multiple of 32."""
@@ -144,6 +159,35 @@ def test_prepared_orientations() -> None:
     assert prepared_orientations(100, 200) == (True, True)    # round8(100) = 104
     assert prepared_orientations(200, 100) == (True, True)
     assert prepared_orientations(72, 72) == (True, True)
+
+
+def test_padded_short_side_never_exceeds_the_long_side() -> None:
+    """Padding a short side that is an odd multiple of 32 to a multiple of 64
+    keeps the iteration's orientation: over square, near-square and ragged
+    shapes, the padded side the iteration treats as short (the unpadded short
+    side) is never longer than the other, both are rounded up to 8 at least, and
+    the library plans the call (launch count from shapes alone, no GPU)."""
+    from dionw_amd.newton_schulz import padded_sides
+
+    sides = [8, 30, 100, 256, 264, 280, 288, 296, 312, 320, 352, 384, 416, 1408, 1440, 1472,
+             2048, 3584]
+    for rows in sides:
+        for cols in sides + [rows + d for d in (1, 8, 31, 32, 33)]:
+            for a, b in ((rows, cols), (cols, rows)):
+                p_pad, j_pad = padded_sides(a, b)
+                assert p_pad >= a and j_pad >= b and p_pad % 8 == 0 and j_pad % 8 == 0
+                r, c = (j_pad, p_pad) if a > b else (p_pad, j_pad)
+                assert r <= c, f"[{a}, {b}] padded to ({p_pad}, {j_pad})"
+                i64 = ctypes.c_int64
+                planned = _lib.library().dionw_newton_schulz_group_launches(
+                    1, (ctypes.c_int32 * 1)(0), (i64 * 1)(1), (i64 * 1)(r), (i64 * 1)(c),
+                    (i64 * 1)(min(a, b)), (i64 * 1)(max(a, b)))
+                assert planned > 0, (a, b)
+    assert padded_sides(288, 288) == (288, 288)
+    assert padded_sides(288, 296) == (288, 296)
+    assert padded_sides(1440, 1440) == (1440, 1440)
+    assert padded_sides(352, 2048) == (384, 2048)   # MoE gate/up iterate: padded
+    assert padded_sides(2048, 352) == (2048, 384)   # its tall twin
 
 
 def test_newton_schulz_needs_the_transpose_it_reads() -> None:
