@@ -43,6 +43,7 @@ from dionw_amd._keys import (
     ParamState,
 )
 from dionw_amd.ema._fusion import ACTIVE_EMA
+from dionw_amd.ema.config import ProfileRegion, no_profile
 from dionw_amd.matrix_update import MomentumForm, RowNormalization
 from dionw_amd.newton_schulz import (
     HipOrthogonalize,
@@ -57,7 +58,19 @@ from dionw_amd.newton_schulz import (
     run_newton_schulz_group,
 )
 
-__all__ = ["ACTIVE_RUNS", "MAX_RUN_ELEMENTS", "RunQueue", "step_run"]
+__all__ = ["ACTIVE_RUNS", "MAX_RUN_ELEMENTS", "PROFILE_REGION", "RunQueue", "step_run"]
+
+# Named regions of a matrix step (host-side ranges around the launches they
+# name, for a profiler's timeline): a run's momentum passes (accumulate, row
+# selection, the prepared Newton-Schulz input), the Newton-Schulz products
+# (one grouped call or one run's), and a run's finish (NorMuon statistics and
+# the weight update).
+MOMENTUM_REGION: Final[str] = "dion_momentum"
+ORTHOGONALIZE_REGION: Final[str] = "dion_orthogonalize"
+FINISH_REGION: Final[str] = "dion_finish"
+# Dion.step binds its ``profile_region`` here for the duration of a step.
+PROFILE_REGION: ContextVar[ProfileRegion] = ContextVar("dionw_amd_profile_region",
+                                                       default=no_profile)
 
 # AdamW update RMS that matrix steps match (Moonshot's 0.2).
 ADAMW_UPDATE_RMS: Final[float] = 0.2
@@ -242,14 +255,17 @@ class RunQueue:
 def _run_lane(calls: list[NewtonSchulzCall], finish: list[Callable[[], None]], lane: list[int],
               grouped: bool, stream: int) -> None:
     """The calls ``lane`` of the queue, then (or each followed by) their runs' passes."""
+    region = PROFILE_REGION.get()
     mine = [calls[i] for i in lane]
     if grouped and len(mine) > 1 and group_launches(mine) < sum(group_launches([c]) for c in mine):
-        run_newton_schulz_group(mine, stream)
+        with region(ORTHOGONALIZE_REGION):
+            run_newton_schulz_group(mine, stream)
         for i in lane:
             finish[i]()
         return
     for i in lane:
-        run_newton_schulz_call(calls[i], stream)
+        with region(ORTHOGONALIZE_REGION):
+            run_newton_schulz_call(calls[i], stream)
         finish[i]()
 
 
@@ -296,33 +312,42 @@ def step_run(
     # Buffers still in use when a queued run finishes get names of their own.
     own = queue.slot(nbytes, stream) if queue is not None else ""
 
-    den = _workspace.buffer(device, "den", (blocks,), torch.float32)
-    rowsq = _workspace.buffer(device, "rowsq", (blocks * rows,), torch.float32)
-    selected = k < rows
-    idx = slot = None
-    if selected:
-        scores = _workspace.buffer(device, "scores", (blocks * rows,), torch.float32)
-        idx = _workspace.buffer(device, "idx" + own, (blocks, k), torch.int32)
-        slot = _workspace.buffer(device, "slot" + own, (blocks, rows), torch.int32)
-        _lib.call("dionw_accumulate_scores", grads, count, per_param * rows, cols,
-                  momentum.data_ptr(), scores.data_ptr(), rowsq.data_ptr(), norm_elem, stream)
-        _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k,
-                  safety, NEWTON_SCHULZ_EPS, idx.data_ptr(), slot.data_ptr(), den.data_ptr(),
-                  norm_elem, stream)
-    elif fused:
-        _lib.call("dionw_full_sumsq", grads, count, per_param * rows, cols, momentum.data_ptr(),
-                  mu, int(nesterov), rowsq.data_ptr(), norm_elem, stream)
-        _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, safety, NEWTON_SCHULZ_EPS,
-                  den.data_ptr(), norm_elem, stream)
-    idx_ptr = None if idx is None else idx.data_ptr()
+    region = PROFILE_REGION.get()
+    with region(MOMENTUM_REGION):
+        den = _workspace.buffer(device, "den", (blocks,), torch.float32)
+        rowsq = _workspace.buffer(device, "rowsq", (blocks * rows,), torch.float32)
+        selected = k < rows
+        idx = slot = None
+        if selected:
+            scores = _workspace.buffer(device, "scores", (blocks * rows,), torch.float32)
+            idx = _workspace.buffer(device, "idx" + own, (blocks, k), torch.int32)
+            slot = _workspace.buffer(device, "slot" + own, (blocks, rows), torch.int32)
+            _lib.call("dionw_accumulate_scores", grads, count, per_param * rows, cols,
+                      momentum.data_ptr(), scores.data_ptr(), rowsq.data_ptr(), norm_elem, stream)
+            _lib.call("dionw_select_rows", scores.data_ptr(), rowsq.data_ptr(), blocks, rows, k,
+                      safety, NEWTON_SCHULZ_EPS, idx.data_ptr(), slot.data_ptr(), den.data_ptr(),
+                      norm_elem, stream)
+        elif fused:
+            _lib.call("dionw_full_sumsq", grads, count, per_param * rows, cols,
+                      momentum.data_ptr(), mu, int(nesterov), rowsq.data_ptr(), norm_elem, stream)
+            _lib.call("dionw_block_denom", rowsq.data_ptr(), blocks, rows, safety,
+                      NEWTON_SCHULZ_EPS, den.data_ptr(), norm_elem, stream)
+        idx_ptr = None if idx is None else idx.data_ptr()
+        if fused:
+            # Only the orientations the iteration reads are written.
+            xr, xt = prepared_inputs(ortho, device, blocks, k, cols, "ns_xr" + own,
+                                     "ns_xt" + own)
+            _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
+                      den.data_ptr(), blocks, rows, cols, k, *padded_sides(k, cols), mu,
+                      int(nesterov), 1, ortho.elem, None if xr is None else xr.data_ptr(),
+                      None if xt is None else xt.data_ptr(), stream)
+        else:
+            raw = torch.empty(blocks, k, cols, device=device, dtype=torch.float32)
+            _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
+                      den.data_ptr(), blocks, rows, cols, k, k, cols, mu, int(nesterov), 1,
+                      _lib.F32, raw.data_ptr(), None, stream)
 
     if fused:
-        # Only the orientations the iteration reads are written.
-        xr, xt = prepared_inputs(ortho, device, blocks, k, cols, "ns_xr" + own, "ns_xt" + own)
-        _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
-                  den.data_ptr(), blocks, rows, cols, k, *padded_sides(k, cols), mu,
-                  int(nesterov), 1, ortho.elem, None if xr is None else xr.data_ptr(),
-                  None if xt is None else xt.data_ptr(), stream)
         orthogonal = _workspace.buffer(device, "ns_out" + own, (blocks, k, cols), torch.bfloat16)
         if queue is not None:
             call = newton_schulz_call(ortho, blocks, k, cols, xr, xt, orthogonal,
@@ -330,14 +355,12 @@ def step_run(
             queue.add(call, partial(_finish_run, run, bucket, positions, group, orthogonal, idx,
                                     slot, step), nbytes, stream, device)
             return
-        run_newton_schulz(ortho, blocks, k, cols, xr, xt, orthogonal, stream)
+        with region(ORTHOGONALIZE_REGION):
+            run_newton_schulz(ortho, blocks, k, cols, xr, xt, orthogonal, stream)
     else:
-        raw = torch.empty(blocks, k, cols, device=device, dtype=torch.float32)
-        _lib.call("dionw_prepare_ns_input", grads, count, momentum.data_ptr(), idx_ptr,
-                  den.data_ptr(), blocks, rows, cols, k, k, cols, mu, int(nesterov), 1,
-                  _lib.F32, raw.data_ptr(), None, stream)
-        orthogonal = ortho(raw, NEWTON_SCHULZ_EPS)
-        orthogonal = orthogonal.to(torch.bfloat16).contiguous()
+        with region(ORTHOGONALIZE_REGION):
+            orthogonal = ortho(raw, NEWTON_SCHULZ_EPS)
+            orthogonal = orthogonal.to(torch.bfloat16).contiguous()
     _finish_run(run, bucket, positions, group, orthogonal, idx, slot, step)
 
 
@@ -354,52 +377,53 @@ def _finish_run(
     """NorMuon statistics and the weight update of a run whose orthogonalized
     rows ``orthogonal`` ([blocks, k, cols] bf16) are ready (_matrix_step.py:274-311),
     on torch's current stream (the queue may finish a run on its second stream)."""
-    device = run.momentum.device
-    stream = _lib.stream_handle(device)
-    blocks, rows, cols, k = run.blocks, bucket.rows, bucket.cols, bucket.selected_rows
-    count = len(run.params)
-    per_param = bucket.blocks_per_param
-    lr = float(group["lr"])
-    idx_ptr = None if idx is None else idx.data_ptr()
-    rowd = scale = None
-    match RowNormalization(group[ROW_NORMALIZATION_KEY]):
-        case RowNormalization.NORMUON:
-            rowd = _workspace.buffer(device, "rowd", (blocks, k), torch.float32)
-            scratch = _workspace.buffer(device, "row_scratch", (2 * blocks * k,), torch.float32)
-            scale = _workspace.buffer(device, "scale", (blocks,), torch.float32)
-            _lib.call("dionw_normuon_stats", orthogonal.data_ptr(), blocks, k, rows, cols,
-                      idx_ptr, run.variance.data_ptr(), float(group[MUON_BETA2_KEY]), step,
-                      rowd.data_ptr(), scratch.data_ptr(), scale.data_ptr(), stream)
-        case RowNormalization.NONE:
-            pass
-        case _ as unreachable:
-            raise RuntimeError(f"no row normalization named {unreachable}")
+    with PROFILE_REGION.get()(FINISH_REGION):
+        device = run.momentum.device
+        stream = _lib.stream_handle(device)
+        blocks, rows, cols, k = run.blocks, bucket.rows, bucket.cols, bucket.selected_rows
+        count = len(run.params)
+        per_param = bucket.blocks_per_param
+        lr = float(group["lr"])
+        idx_ptr = None if idx is None else idx.data_ptr()
+        rowd = scale = None
+        match RowNormalization(group[ROW_NORMALIZATION_KEY]):
+            case RowNormalization.NORMUON:
+                rowd = _workspace.buffer(device, "rowd", (blocks, k), torch.float32)
+                scratch = _workspace.buffer(device, "row_scratch", (2 * blocks * k,), torch.float32)
+                scale = _workspace.buffer(device, "scale", (blocks,), torch.float32)
+                _lib.call("dionw_normuon_stats", orthogonal.data_ptr(), blocks, k, rows, cols,
+                          idx_ptr, run.variance.data_ptr(), float(group[MUON_BETA2_KEY]), step,
+                          rowd.data_ptr(), scratch.data_ptr(), scale.data_ptr(), stream)
+            case RowNormalization.NONE:
+                pass
+            case _ as unreachable:
+                raise RuntimeError(f"no row normalization named {unreachable}")
 
-    weight_decay = float(group["weight_decay"])
-    decay = 1.0 - lr * weight_decay
-    common = (count, per_param, rows, cols, k, orthogonal.data_ptr(), idx_ptr,
-              None if slot is None else slot.data_ptr(), None if rowd is None else rowd.data_ptr(),
-              None if scale is None else scale.data_ptr(), step, decay, int(weight_decay > 0.0))
-    # A due GPU EMA lerp of these weights rides on the apply pass (one pass
-    # instead of apply then EMA; the same lerp arithmetic).
-    ema = ACTIVE_EMA.get()
-    params = [bucket.params[i] for i in positions]
-    fusable = ema is not None and not run.writeback
-    shadows = ema.fusable_shadows(params) if fusable else None
-    # A due CPU EMA's host snapshots may be written by the same pass (the new
-    # weights go to HBM and over the host link at once) instead of copied after it.
-    staged = ema.stageable_buffers(params) if fusable and ema.fuse_host_copies else None
-    if shadows is not None:
-        _lib.call("dionw_apply_update_ema", _lib.ptr_array(run.params), _lib.ptr_array(shadows),
-                  *common, ema.fused_weight(), stream)
-        ema.mark_fused(params)
-    elif staged is not None:
-        _lib.call("dionw_apply_update_stage", _lib.ptr_array(run.params),
-                  _lib.ptr_array(staged), *common, stream)
-        ema.mark_staged(params)
-    else:
-        _lib.call("dionw_apply_update", _lib.ptr_array(run.params), *common, stream)
-    for param, copy in run.writeback:
-        param.copy_(copy)
-    if ema is not None:
-        ema.stage_written(params)
+        weight_decay = float(group["weight_decay"])
+        decay = 1.0 - lr * weight_decay
+        common = (count, per_param, rows, cols, k, orthogonal.data_ptr(), idx_ptr,
+                  None if slot is None else slot.data_ptr(), None if rowd is None else rowd.data_ptr(),
+                  None if scale is None else scale.data_ptr(), step, decay, int(weight_decay > 0.0))
+        # A due GPU EMA lerp of these weights rides on the apply pass (one pass
+        # instead of apply then EMA; the same lerp arithmetic).
+        ema = ACTIVE_EMA.get()
+        params = [bucket.params[i] for i in positions]
+        fusable = ema is not None and not run.writeback
+        shadows = ema.fusable_shadows(params) if fusable else None
+        # A due CPU EMA's host snapshots may be written by the same pass (the new
+        # weights go to HBM and over the host link at once) instead of copied after it.
+        staged = ema.stageable_buffers(params) if fusable and ema.fuse_host_copies else None
+        if shadows is not None:
+            _lib.call("dionw_apply_update_ema", _lib.ptr_array(run.params), _lib.ptr_array(shadows),
+                      *common, ema.fused_weight(), stream)
+            ema.mark_fused(params)
+        elif staged is not None:
+            _lib.call("dionw_apply_update_stage", _lib.ptr_array(run.params),
+                      _lib.ptr_array(staged), *common, stream)
+            ema.mark_staged(params)
+        else:
+            _lib.call("dionw_apply_update", _lib.ptr_array(run.params), *common, stream)
+        for param, copy in run.writeback:
+            param.copy_(copy)
+        if ema is not None:
+            ema.stage_written(params)

@@ -21,10 +21,19 @@ import math
 
 import torch
 
-__all__ = ["buffer", "release", "held_bytes"]
+__all__ = ["buffer", "release", "held_bytes", "share", "tensors"]
 
 _ALIGN = 256
 _BUFFERS: dict[tuple[torch.device, int, str], torch.Tensor] = {}
+
+
+def _resolved(device: torch.device | str) -> torch.device:
+    """``device`` with its index filled in: ``cuda`` means the current GPU, so
+    that ``cuda`` and ``cuda:0`` name the same buffers when GPU 0 is current."""
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    return device
 
 
 def _stream_of(device: torch.device) -> int:
@@ -44,7 +53,7 @@ def buffer(device: torch.device, name: str, shape: tuple[int, ...], dtype: torch
            stream: int | None = None) -> torch.Tensor:
     """A ``shape`` view of the named scratch buffer of ``device`` and ``stream``
     (torch's current stream on ``device`` when None); uninitialized."""
-    device = torch.device(device)
+    device = _resolved(device)
     stream = _stream_of(device) if stream is None else stream
     numel = math.prod(shape)
     nbytes = max(numel * torch.empty((), dtype=dtype).element_size(), 1)
@@ -61,11 +70,33 @@ def buffer(device: torch.device, name: str, shape: tuple[int, ...], dtype: torch
 
 def release(device: torch.device | None = None) -> None:
     """Drop the scratch buffers (of ``device``, or all)."""
-    for key in [k for k in _BUFFERS if device is None or k[0] == torch.device(device)]:
+    device = None if device is None else _resolved(device)
+    for key in [k for k in _BUFFERS if device is None or k[0] == device]:
         _retire(_BUFFERS.pop(key), key[1])
 
 
 def held_bytes(device: torch.device | None = None) -> int:
     """Bytes held by the scratch buffers (of ``device``, or all)."""
-    return sum(t.numel() for k, t in _BUFFERS.items()
-               if device is None or k[0] == torch.device(device))
+    device = None if device is None else _resolved(device)
+    unique = {t.data_ptr(): t.numel() for k, t in _BUFFERS.items()
+              if device is None or k[0] == device}
+    return sum(unique.values())
+
+
+def share(device: torch.device, source: int, target: int) -> None:
+    """Let work on stream ``target`` use the buffers of stream ``source``
+    (names it has none of yet). For a stream that only records launches made
+    in stream order with ``source``'s, such as a graph capture stream whose
+    replays run on ``source``: the recorded launches then use the same scratch
+    as eager steps instead of a second copy."""
+    device = _resolved(device)
+    for (dev, stream, name), store in list(_BUFFERS.items()):
+        if dev == device and stream == source:
+            _BUFFERS.setdefault((dev, target, name), store)
+
+
+def tensors(device: torch.device | None = None) -> list[torch.Tensor]:
+    """The scratch buffers held now (of ``device``, or all), e.g. to keep them
+    alive for launches recorded in a graph."""
+    device = None if device is None else _resolved(device)
+    return [t for k, t in _BUFFERS.items() if device is None or k[0] == device]

@@ -43,13 +43,23 @@ from dionw_amd._keys import (
     ROUTE_KEY,
     ROW_NORMALIZATION_KEY,
 )
-from dionw_amd._matrix_step import ACTIVE_RUNS, MAX_RUN_ELEMENTS, RunQueue, step_run
+from dionw_amd._matrix_step import (
+    ACTIVE_RUNS,
+    MAX_RUN_ELEMENTS,
+    PROFILE_REGION,
+    RunQueue,
+    step_run,
+)
 from dionw_amd.ema import EMAConfig, IntegratedEMAOptimizer, ProfileRegion, no_profile
 from dionw_amd.ema._fusion import ACTIVE_EMA
 from dionw_amd.matrix_update import DION3_UPDATE, MatrixUpdate
 from dionw_amd.routing import RouteKind
 
-__all__ = ["MAX_RUN_ELEMENTS", "NEWTON_SCHULZ_KEY", "Dion", "step_run"]
+__all__ = ["ADAMW_REGION", "MAX_RUN_ELEMENTS", "NEWTON_SCHULZ_KEY", "Dion", "step_run"]
+
+# The named region around a step's AdamW groups (the matrix stages name theirs
+# in _matrix_step; the EMA's are the tracker's).
+ADAMW_REGION = "adamw"
 
 _T = TypeVar("_T")
 
@@ -131,6 +141,7 @@ class Dion(IntegratedEMAOptimizer):
             ROW_NORMALIZATION_KEY: matrix_update.row_normalization.value,
             MOMENTUM_FORM_KEY: matrix_update.momentum_form.value,
         })
+        self._profile_region = profile_region
         self._init_integrated_ema(ema, profile_region)
 
     # -- groups and state ------------------------------------------------------
@@ -197,6 +208,28 @@ class Dion(IntegratedEMAOptimizer):
             self._packed = pack_buckets(self.param_groups, self.state)
         return self._packed
 
+    def _check_capturable(self) -> None:
+        """Refuse a step under HIP graph capture that a replay would not repeat.
+
+        A captured step replays the launches of the step it recorded: its
+        gradient tensors, hyperparameters and step sizes. Two things a step
+        can do are not launches and must not be recorded: packing the matrix
+        state (zeroed buckets and copies of earlier state, after construction,
+        ``add_param_group`` or ``load_state_dict``), which a replay would redo
+        on every step, and the EMA's host-side schedule.
+
+        Raises:
+            RuntimeError: If the state is not packed or an EMA is attached.
+        """
+        if self._packed is None:
+            raise RuntimeError(
+                "Dion.step under graph capture: the matrix state is not packed (the first step "
+                "after construction, add_param_group or load_state_dict packs it); run one "
+                "eager step first, or call initialize_state on a matrix parameter")
+        if self.ema is not None:
+            raise RuntimeError("Dion.step under graph capture: the EMA's schedule runs on the "
+                               "host each step and cannot be replayed; capture without an EMA")
+
     # -- the step ----------------------------------------------------------------
     @torch.no_grad()
     def step(self, closure: Callable[[], float] | None = None) -> float | None:  # type: ignore[override]
@@ -205,20 +238,27 @@ class Dion(IntegratedEMAOptimizer):
         Raises:
             RuntimeError: If the EMA weights are in the parameters.
         """
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            self._check_capturable()
         with self._ema_cadence():
             loss = None
             if closure is not None:
                 with torch.enable_grad():
                     loss = closure()
             queue = RunQueue()
-            with _bound(ACTIVE_EMA, self.ema), _bound(ACTIVE_RUNS, queue):
+            region = self._profile_region
+            with (_bound(ACTIVE_EMA, self.ema), _bound(ACTIVE_RUNS, queue),
+                  _bound(PROFILE_REGION, region)):
                 for bucket in self._buckets():
                     group = self.param_groups[bucket.group_index]
                     for positions in _runs(bucket):
                         step_run(bucket, positions, group, self.state)
                 queue.flush()
-                for group in self.param_groups:
-                    if group[ROUTE_KEY] == RouteKind.ADAMW.value:
-                        adamw_step(group, self.state)
+                adamw_groups = [g for g in self.param_groups
+                                if g[ROUTE_KEY] == RouteKind.ADAMW.value]
+                if adamw_groups:
+                    with region(ADAMW_REGION):
+                        for group in adamw_groups:
+                            adamw_step(group, self.state)
         return loss
 

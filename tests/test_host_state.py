@@ -179,3 +179,87 @@ def test_workspace_is_keyed_by_device_and_stream() -> None:
     import dionw_amd
     dionw_amd.release_workspace(cpu)  # the public name of the same release
     assert _workspace.held_bytes(cpu) == 0
+
+
+def test_workspace_release_resolves_the_current_gpu(monkeypatch) -> None:
+    """``cuda`` names the current GPU: buffers kept under ``cuda:0`` are counted
+    and released through ``cuda`` as well (an index-less device must not match
+    nothing). A CPU tensor stands in for the GPU buffer; nothing is launched."""
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    assert _workspace._resolved("cuda") == torch.device("cuda", 0)
+    assert _workspace._resolved("cuda:1") == torch.device("cuda", 1)
+    assert _workspace._resolved("cpu") == torch.device("cpu")
+    key = (torch.device("cuda", 0), 0, "stand_in")
+    monkeypatch.setitem(_workspace._BUFFERS, key, torch.zeros(512, dtype=torch.uint8))
+    assert _workspace.held_bytes("cuda") >= 512
+    assert _workspace.held_bytes(torch.device("cuda", 1)) == 0
+    import dionw_amd
+    dionw_amd.release_workspace("cuda")
+    assert key not in _workspace._BUFFERS and _workspace.held_bytes("cuda") == 0
+
+
+def test_step_stages_run_in_named_regions_in_step_order(monkeypatch) -> None:
+    """``profile_region`` marks every stage of a step, in step order: each run's
+    momentum passes, then the queued Newton-Schulz products, each run's finish
+    (NorMuon statistics and the weight update), then the AdamW groups. The
+    library calls are recorded instead of executed (CPU tensors stand in for
+    GPU ones, nothing is launched), so the test also pins which entry points
+    each stage issues."""
+    import contextlib
+
+    from dionw_amd import _groups, _lib, _matrix_step
+
+    events: list[tuple[str, str]] = []
+    depth = []
+
+    @contextlib.contextmanager
+    def region(name: str):
+        assert not depth, f"region {name} opened inside {depth[-1]}"
+        depth.append(name)
+        events.append(("region", name))
+        try:
+            yield
+        finally:
+            depth.pop()
+
+    def record(name: str, *args) -> None:
+        events.append(("call", name))
+
+    monkeypatch.setattr(_lib, "call", record)
+    monkeypatch.setattr(_lib, "stream_handle", lambda device=None: 0)
+    monkeypatch.setattr(_groups, "check_parameter", lambda param: None)
+    monkeypatch.setattr(opt_module, "check_parameter", lambda param: None)
+    # One stream for the flush (a second one would need a GPU).
+    monkeypatch.setattr(_matrix_step, "_lanes", lambda calls, grouped: [list(range(len(calls)))])
+    g = torch.Generator().manual_seed(0)
+    wide = [nn.Parameter(torch.randn(64, 256, generator=g)) for _ in range(2)]
+    wider = nn.Parameter(torch.randn(64, 512, generator=g))
+    bias = nn.Parameter(torch.zeros(64))
+    opt = opt_module.Dion(
+        [{"params": [*wide, wider], "dion_route": "matrix", "fraction": 0.25},
+         {"params": [bias], "dion_route": "adamw"}],
+        lr=1e-3, profile_region=region)
+    for p in (*wide, wider, bias):
+        p.grad = torch.randn(p.shape, generator=g)
+    opt.step()
+    regions = [name for kind, name in events if kind == "region"]
+    # Two buckets (64x256 and 64x512 blocks): momentum passes per run, then
+    # the queue's products (grouped or one call per run) and each run's finish.
+    assert regions[:2] == ["dion_momentum", "dion_momentum"]
+    assert regions[-1] == "adamw"
+    middle = regions[2:-1]
+    assert middle.count("dion_finish") == 2 and "dion_orthogonalize" in middle
+    assert middle.index("dion_orthogonalize") < middle.index("dion_finish")
+    stage = None
+    issued: dict[str, set[str]] = {}
+    for kind, name in events:
+        if kind == "region":
+            stage = name
+        else:
+            assert stage is not None, f"{name} issued outside every region"
+            issued.setdefault(stage, set()).add(name)
+    assert issued["dion_momentum"] == {"dionw_accumulate_scores", "dionw_select_rows",
+                                       "dionw_prepare_ns_input"}
+    assert issued["dion_orthogonalize"] <= {"dionw_newton_schulz", "dionw_newton_schulz_group"}
+    assert issued["dion_finish"] == {"dionw_normuon_stats", "dionw_apply_update"}
+    assert issued["adamw"] == {"dionw_increment_steps", "dionw_adamw"}
