@@ -33,6 +33,8 @@ from dionw_amd.routing import Route, RouteKind, RouteProvider
 # Not in the reference: frees the device scratch the HIP passes keep between steps
 # (it grows to the largest run queued; a later step allocates it again).
 from dionw_amd._workspace import release as release_workspace  # noqa: F401
+# Not in the reference: one step recorded as a HIP graph and replayed.
+from dionw_amd.graph import StepGraph  # noqa: F401
 
 __version__ = "0.1.0"
 
