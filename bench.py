@@ -527,21 +527,50 @@ def cpu_baseline(spec, fraction: float, share: dict) -> dict:
 GPU_BUSY_CYCLES = 200_000_000
 
 
-def host_dispatch_ms(torch, opt, samples: int = 7) -> float:
-    """Median host time of one ``opt.step()`` while the GPU is held busy
-    (reference bench/host_dispatch.py:28-56): the Python and launch overhead
-    alone, independent of how many steps are timed."""
+def host_dispatch_ms(torch, opt, samples: int = 7, call=None) -> float:
+    """Median host time of one ``opt.step()`` (or ``call``) while the GPU is
+    held busy (reference bench/host_dispatch.py:28-56): the Python and launch
+    overhead alone, independent of how many steps are timed."""
     import statistics
 
+    call = opt.step if call is None else call
     times = []
     for _ in range(samples):
         torch.cuda.synchronize()
         torch.cuda._sleep(GPU_BUSY_CYCLES)
         start = time.perf_counter()
-        opt.step()
+        call()
         times.append((time.perf_counter() - start) * 1e3)
     torch.cuda.synchronize()
     return statistics.median(times)
+
+
+def step_graph_report(torch, opt, steps: int) -> dict:
+    """A ``StepGraph`` of the optimizer against its eager steps, same process:
+    GPU ms per step of each (HIP events, three alternating rounds of ``steps``)
+    and the host ms of one call with the GPU held busy."""
+    from dionw_amd import StepGraph
+
+    graph = StepGraph(opt)
+    graph.replay()
+
+    def timed(call) -> float:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            call()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    rounds = [(timed(opt.step), timed(graph.replay)) for _ in range(3)]
+    return {
+        "eager_ms": [round(e, 3) for e, _ in rounds],
+        "replay_ms": [round(r, 3) for _, r in rounds],
+        "eager_host_ms": round(host_dispatch_ms(torch, opt), 3),
+        "replay_host_ms": round(host_dispatch_ms(torch, opt, call=graph.replay), 3),
+    }
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
@@ -571,6 +600,42 @@ def traffic_bytes():
         return data["ns_step"]["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def state_bytes(opt) -> int:
+    """Bytes of the optimizer's state tensors (each storage once: bucket views
+    share their bucket's storage)."""
+    seen: dict[int, int] = {}
+    for state in opt.state.values():
+        for value in state.values():
+            if hasattr(value, "untyped_storage") and value.is_cuda:
+                storage = value.untyped_storage()
+                seen[storage.data_ptr()] = storage.nbytes()
+    return sum(seen.values())
+
+
+def memory_report(torch, opt, before_optimizer: int) -> dict:
+    """The step's device memory above the parameters, gradients and optimizer
+    state, from torch's allocator: ``scratch_held_gb`` is what the HIP passes
+    keep between steps (named scratch buffers, regrown on demand), and
+    ``peak_above_state_gb`` the peak of one more step above parameters,
+    gradients and state (held scratch included) — the figure the reference
+    quotes for its runs (src/dionw/_matrix_step.py:44-49)."""
+    from dionw_amd import _workspace
+
+    torch.cuda.synchronize()
+    state = state_bytes(opt)
+    held = _workspace.held_bytes()
+    torch.cuda.reset_peak_memory_stats()
+    opt.step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated()
+    return {
+        "state_gb": round(state / 1e9, 3),
+        "scratch_held_gb": round(held / 1e9, 3),
+        "peak_above_state_gb": round((peak - before_optimizer - state) / 1e9, 3),
+        "device_peak_gb": round(peak / 1e9, 3),
+    }
 
 
 def probe() -> int:
@@ -628,6 +693,8 @@ def main() -> int:
                                  "transformer-1.34b", "ns-wide"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--instrumented-steps", type=int, default=2)
+    parser.add_argument("--step-graph", action="store_true",
+                        help="also time replays of the step recorded as a HIP graph (no EMA)")
     args = parser.parse_args()
     if args.probe:
         return probe()
@@ -667,6 +734,8 @@ def main() -> int:
         else:
             groups = [{"params": experts, "dion_route": "matrix", "fraction": 1.0}]
             kwargs["matrix_update"] = dionw_amd.MUON_UPDATE
+    torch.cuda.synchronize()
+    before_optimizer = torch.cuda.memory_allocated()  # parameters and gradients
     opt = dionw_amd.Dion(groups, lr=3e-4, weight_decay=0.05, momentum=0.95, muon_beta2=0.95,
                          betas=(0.9, 0.95), eps=1e-8, **kwargs)
     torch.cuda.synchronize()
@@ -701,6 +770,16 @@ def main() -> int:
                      **({"gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)} if v["bytes"] else {})}
               for name, v in sorted(summary.items(), key=lambda kv: -kv[1]["ms"])}
     print(f"[bench] phases {json.dumps(phases)}", file=sys.stderr, flush=True)
+    memory = memory_report(torch, opt, before_optimizer)
+    print(f"[bench] memory {json.dumps(memory)}", file=sys.stderr, flush=True)
+    graph = None
+    if args.step_graph:
+        if opt.ema is not None:
+            print("[bench] --step-graph: the EMA config cannot be recorded; skipped",
+                  file=sys.stderr, flush=True)
+        else:
+            graph = step_graph_report(torch, opt, args.steps)
+            print(f"[bench] step graph {json.dumps(graph)}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline and args.config == "llama3-8b":
@@ -746,6 +825,8 @@ def main() -> int:
                               "peak": PEAK_HBM_GBS, "unit": "GB/s",
                               "frac": round(acc_gbs / PEAK_HBM_GBS, 4)} if acc_gbs else None,
         "host_dispatch_ms": round(host_dispatch, 3),
+        "memory": memory,
+        **({"step_graph": graph} if graph is not None else {}),
         "phases": phases,
         "roofline": {
             "bound": "mfma",

@@ -208,12 +208,28 @@ class RunQueue:
         self._stream: int | None = None
         self._device: torch.device | None = None
 
-    def slot(self, nbytes: int, stream: int) -> str:
-        """Name suffix of the next run's buffers; flushes first if that run does not fit."""
+    def slot(self, nbytes: int, stream: int, device: torch.device) -> str:
+        """Name suffix of the next run's buffers; flushes first if that run does not fit.
+
+        The buffers of queue position ``#i`` are kept from one flush (and step)
+        to the next. If growing this position's to ``nbytes`` would take the
+        kept total past ``QUEUE_BYTES``, the queue is flushed and every
+        position's buffers are dropped first, so the buffers kept never exceed
+        ``QUEUE_BYTES`` (or one run's, where a run alone is larger).
+        """
         if self._calls and (len(self._calls) >= QUEUE_RUNS or stream != self._stream
                             or self._bytes + nbytes > QUEUE_BYTES):
             self.flush()
-        return f"#{len(self._calls)}"
+        own = f"#{len(self._calls)}"
+        kept = _workspace.named_bytes(device, stream, _queued_name)
+        mine = _workspace.named_bytes(device, stream,
+                                      lambda name: name.partition("#")[2] == own[1:])
+        others = kept - mine
+        if others > 0 and others + max(mine, nbytes) > QUEUE_BYTES:
+            self.flush()
+            _workspace.release_named(device, stream, _queued_name)
+            own = "#0"
+        return own
 
     def add(self, call: NewtonSchulzCall, finish: Callable[[], None], nbytes: int,
             stream: int, device: torch.device) -> None:
@@ -269,6 +285,11 @@ def _run_lane(calls: list[NewtonSchulzCall], finish: list[Callable[[], None]], l
         finish[i]()
 
 
+def _queued_name(name: str) -> bool:
+    """Whether a scratch buffer belongs to a queue position (``#i`` suffix)."""
+    return "#" in name
+
+
 def _ns_bytes(ortho: HipOrthogonalize, blocks: int, k: int, cols: int) -> int:
     """Bytes of a fused run's Newton-Schulz buffers (inputs, output, workspace)."""
     p_pad, j_pad = padded_sides(k, cols)
@@ -310,7 +331,7 @@ def step_run(
     queue = ACTIVE_RUNS.get() if fused else None
     nbytes = _ns_bytes(ortho, blocks, k, cols) if queue is not None else 0
     # Buffers still in use when a queued run finishes get names of their own.
-    own = queue.slot(nbytes, stream) if queue is not None else ""
+    own = queue.slot(nbytes, stream, device) if queue is not None else ""
 
     region = PROFILE_REGION.get()
     with region(MOMENTUM_REGION):

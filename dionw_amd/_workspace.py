@@ -10,18 +10,20 @@ touches comes from here or from the optimizer state.
 
 ``release`` drops the buffers (the optimizer calls it when its packing
 changes); they are recreated on demand. A queued step keeps one buffer set per
-queued run (names with a ``#i`` suffix) until its grouped orthogonalization
-has run, so the peak is the sum over the runs of one flush: at most the queue's
-byte cap plus the largest run.
+queue position (names with a ``#i`` suffix), reused from one flush and one step
+to the next; the queue drops them all before their total would pass its byte
+cap, so they hold at most that cap, or one run's set where a run alone is
+larger.
 """
 
 from __future__ import annotations
 
 import math
+from collections.abc import Callable
 
 import torch
 
-__all__ = ["buffer", "release", "held_bytes", "share", "tensors"]
+__all__ = ["buffer", "release", "release_named", "held_bytes", "named_bytes", "share", "tensors"]
 
 _ALIGN = 256
 _BUFFERS: dict[tuple[torch.device, int, str], torch.Tensor] = {}
@@ -72,6 +74,20 @@ def release(device: torch.device | None = None) -> None:
     """Drop the scratch buffers (of ``device``, or all)."""
     device = None if device is None else _resolved(device)
     for key in [k for k in _BUFFERS if device is None or k[0] == device]:
+        _retire(_BUFFERS.pop(key), key[1])
+
+
+def named_bytes(device: torch.device, stream: int, match: Callable[[str], bool]) -> int:
+    """Bytes held by the buffers of ``device`` and ``stream`` whose names ``match``."""
+    device = _resolved(device)
+    return sum(t.numel() for (dev, st, name), t in _BUFFERS.items()
+               if dev == device and st == stream and match(name))
+
+
+def release_named(device: torch.device, stream: int, match: Callable[[str], bool]) -> None:
+    """Drop the buffers of ``device`` and ``stream`` whose names ``match``."""
+    device = _resolved(device)
+    for key in [k for k in _BUFFERS if k[0] == device and k[1] == stream and match(k[2])]:
         _retire(_BUFFERS.pop(key), key[1])
 
 

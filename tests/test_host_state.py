@@ -263,3 +263,44 @@ def test_step_stages_run_in_named_regions_in_step_order(monkeypatch) -> None:
     assert issued["dion_orthogonalize"] <= {"dionw_newton_schulz", "dionw_newton_schulz_group"}
     assert issued["dion_finish"] == {"dionw_normuon_stats", "dionw_apply_update"}
     assert issued["adamw"] == {"dionw_increment_steps", "dionw_adamw"}
+
+
+def test_queue_keeps_at_most_its_byte_cap(monkeypatch) -> None:
+    """The queue's per-position scratch is reused across flushes and steps, and
+    dropped before growing one position would take the total past the byte cap:
+    what it keeps stays within the cap, or one run's buffers when a run alone is
+    larger. CPU buffers stand in for the GPU's; the products are not launched."""
+    from dionw_amd import _matrix_step
+    from dionw_amd._matrix_step import RunQueue
+
+    cpu = torch.device("cpu")
+    monkeypatch.setattr(_matrix_step, "QUEUE_BYTES", 10_000)
+    monkeypatch.setattr(_matrix_step, "group_launches", lambda calls: len(calls))
+    monkeypatch.setattr(_matrix_step, "run_newton_schulz_call", lambda call, stream: None)
+    monkeypatch.setattr(_matrix_step, "run_newton_schulz_group", lambda calls, stream: None)
+    monkeypatch.setattr(_matrix_step, "_lanes", lambda calls, grouped: [list(range(len(calls)))])
+    _workspace.release(cpu)
+    queue = RunQueue()
+    kept = lambda: _workspace.named_bytes(cpu, 0, lambda name: "#" in name)  # noqa: E731
+
+    def run(nbytes: int) -> str:
+        own = queue.slot(nbytes, 0, cpu)
+        _workspace.buffer(cpu, "ns_out" + own, (nbytes,), torch.uint8, stream=0)
+        queue.add(object(), lambda: None, nbytes, 0, cpu)
+        return own
+
+    assert [run(3000) for _ in range(3)] == ["#0", "#1", "#2"]
+    queue.flush()
+    assert kept() <= 10_000
+    # Growing position 0 to 9000 next to 6000 kept elsewhere would pass the cap:
+    # every position's buffers are dropped first.
+    assert run(9000) == "#0" and kept() <= 10_000
+    assert run(3000) == "#0"  # does not fit beside the 9000 queued: flushed, reused
+    queue.flush()
+    assert kept() <= 10_000
+    # A run larger than the cap alone: kept, nothing else beside it.
+    assert run(25_000) == "#0" and 25_000 <= kept() < 25_000 + 256  # 256-byte alignment
+    queue.flush()
+    assert run(100) == "#0" and kept() < 25_000 + 256
+    queue.flush()
+    _workspace.release(cpu)
