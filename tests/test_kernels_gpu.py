@@ -342,11 +342,15 @@ def _check_symmetric(dtype: torch.dtype, shape: tuple[int, ...]) -> None:
 
 
 # Short sides that are multiples of 32 read the iterate directly in the left
-# products; the others (40, 72, 104) read its transpose. Ragged ones pad; an
-# odd multiple of 32 (288) next to a long side less than 32 longer stays unpadded.
+# products; the others (40, 72, 104, 1400) read its transpose. Ragged ones pad;
+# an odd multiple of 32 (288) next to a long side less than 32 longer stays
+# unpadded.
 NS_SHAPES = [(3, 64, 256), (3, 256, 64), (3, 128, 128), (2, 96, 160), (4, 256, 1024), (1, 352, 2048),
              (2, 30, 300), (2, 300, 30), (2, 40, 200), (2, 200, 40), (1, 72, 72), (2, 100, 520),
-             (1, 288, 296), (1, 296, 288), (1, 288, 288)]
+             (1, 288, 296), (1, 296, 288), (1, 288, 288),
+             # Sides with a ragged last 256-row tile (MoE-Muon's 1408 = 5 x 256 + 128;
+             # 1400, whose transpose is read), wide, tall and square.
+             (1, 1408, 2048), (1, 2048, 1408), (1, 1400, 1600), (1, 1408, 1408)]
 
 # Each kind's polynomials and norm safety (what its rounding is measured against).
 POLYNOMIALS = {
