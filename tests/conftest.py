@@ -19,18 +19,9 @@ if str(ROOT) not in sys.path:
 
 def pytest_configure(config: pytest.Config) -> None:
     config.addinivalue_line("markers", "gpu: needs an MI355X GPU and the built HIP library")
-    config.addinivalue_line("markers", "bench: performance claims on an idle MI355X; run only "
-                            "with DIONW_BENCH=1 (python -m pytest tests -m bench)")
 
 
 def pytest_collection_modifyitems(config: pytest.Config, items: list[pytest.Item]) -> None:
-    import os
-
-    benching = os.environ.get("DIONW_BENCH") == "1" and torch.cuda.is_available()
-    skip_bench = pytest.mark.skip(reason="performance claims run only with DIONW_BENCH=1 on a GPU")
-    for item in items:
-        if "bench" in item.keywords and not benching:
-            item.add_marker(skip_bench)
     if torch.cuda.is_available():
         return
     skip = pytest.mark.skip(reason="no GPU on this host")
