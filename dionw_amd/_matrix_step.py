@@ -423,8 +423,8 @@ def _finish_run(
         weight_decay = float(group["weight_decay"])
         decay = 1.0 - lr * weight_decay
         common = (count, per_param, rows, cols, k, orthogonal.data_ptr(), idx_ptr,
-                  None if slot is None else slot.data_ptr(), None if rowd is None else rowd.data_ptr(),
-                  None if scale is None else scale.data_ptr(), step, decay, int(weight_decay > 0.0))
+                  _lib.ptr(slot), _lib.ptr(rowd), _lib.ptr(scale), step, decay,
+                  int(weight_decay > 0.0))
         # A due GPU EMA lerp of these weights rides on the apply pass (one pass
         # instead of apply then EMA; the same lerp arithmetic).
         ema = ACTIVE_EMA.get()

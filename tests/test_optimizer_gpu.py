@@ -210,7 +210,8 @@ def test_release_workspace_by_index_less_device_frees_the_step_scratch() -> None
     opt.step()
     torch.cuda.synchronize()
     assert _workspace.held_bytes("cuda") > 0
-    assert _workspace.held_bytes("cuda") == _workspace.held_bytes(f"cuda:{torch.cuda.current_device()}")
+    here = f"cuda:{torch.cuda.current_device()}"
+    assert _workspace.held_bytes("cuda") == _workspace.held_bytes(here)
     dionw_amd.release_workspace("cuda")
     assert _workspace.held_bytes("cuda") == 0
     opt.step()

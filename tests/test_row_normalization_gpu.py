@@ -45,7 +45,8 @@ def _normalize_rows_float64(o: torch.Tensor, variance: torch.Tensor, beta2: floa
     u, v = o.double(), variance.double()
     v = v + (u.square().mean(-1, keepdim=True) - v) * (1.0 - beta2)
     n = u / (v.sqrt() + 1e-8)
-    restore = u.norm(dim=(-2, -1), keepdim=True) / n.norm(dim=(-2, -1), keepdim=True).clamp_min(1e-8)
+    new_norm = n.norm(dim=(-2, -1), keepdim=True).clamp_min(1e-8)
+    restore = u.norm(dim=(-2, -1), keepdim=True) / new_norm
     return n * (restore * step)
 
 
@@ -125,7 +126,8 @@ def test_finish_equals_the_fused_step(monkeypatch, shape, fraction, weight_decay
     for it in range(2):
         param.grad = (torch.randn(*shape, generator=g) * 1e-3).to(DEV)
         before = param.detach().clone()
-        var_before = opt.state[param]["variance"].clone() if it else torch.zeros(rows, 1, device=DEV)
+        var_before = (opt.state[param]["variance"].clone() if it
+                      else torch.zeros(rows, 1, device=DEV))
         recorded.clear()
         opt.step()
         torch.cuda.synchronize()
