@@ -63,7 +63,9 @@ CASES = [((256, 512), 0.25), ((64, 128), 1.0), ((64, 128), 0.5), ((256, 64), 0.5
          ((128, 128), 0.25), ((160, 96), 1.0),
          # sides that are not multiples of 8 or 4 (padded Newton-Schulz input,
          # scalar row loads), and a long block (16384 rows, top-4096 selection)
-         ((100, 70), 0.3), ((37, 61), 1.0), ((16384, 128), 0.25)]
+         ((100, 70), 0.3), ((37, 61), 1.0), ((16384, 128), 0.25),
+         # a single selected row (k = 1), and a single-row block
+         ((64, 128), 1.0 / 64), ((1, 96), 1.0)]
 
 
 @pytest.mark.parametrize("weight_decay", [0.0, 0.1])
@@ -110,7 +112,9 @@ def _exact_polar_cpu(x: torch.Tensor, epsilon: float) -> torch.Tensor:
     # longer (no padding to 64-deep stages): square, near-square (where Gram's
     # rounding error is ~1.6e-2), tall, and a selected k = 288 beside 296 columns.
     ((288, 288), 1.0, None), ((288, 296), 1.0, None), ((296, 288), 1.0, None),
-    ((1152, 296), 0.25, None)])
+    ((1152, 296), 0.25, None),
+    # one selected row: a 1 x 128 iterate (padded to 8 rows)
+    ((64, 128), 1.0 / 64, None)])
 def test_hip_step_matches_oracle(kind, shape, fraction, heads) -> None:
     """The full HIP step (Newton-Schulz included) against the oracle: selection
     and momentum bit-exact, parameters within the north-star 2e-3, and the
