@@ -181,6 +181,31 @@ def test_workspace_is_keyed_by_device_and_stream() -> None:
     assert _workspace.held_bytes(cpu) == 0
 
 
+def test_workspace_share_aliases_only_missing_names() -> None:
+    """A capture stream sees the eager stream's buffers (same storage), keeps
+    the ones it already has, and a shared buffer is counted once."""
+    cpu = torch.device("cpu")
+    _workspace.release(cpu)
+    a = _workspace.buffer(cpu, "a", (64,), torch.float32, stream=1)
+    _workspace.buffer(cpu, "b", (64,), torch.float32, stream=1)
+    own = _workspace.buffer(cpu, "b", (8,), torch.float32, stream=2)
+    before = _workspace.held_bytes(cpu)
+    _workspace.share(cpu, 1, 2)
+    assert _workspace.buffer(cpu, "a", (64,), torch.float32, stream=2).data_ptr() == a.data_ptr()
+    assert _workspace.buffer(cpu, "b", (8,), torch.float32, stream=2).data_ptr() == own.data_ptr()
+    assert _workspace.held_bytes(cpu) == before
+    assert len(_workspace.tensors(cpu)) == 4  # (1, a), (1, b), (2, b), (2, a)
+    _workspace.release(cpu)
+    assert _workspace.tensors(cpu) == []
+
+
+def test_step_graph_records_only_a_dion() -> None:
+    from dionw_amd import StepGraph
+    param = nn.Parameter(torch.zeros(4, 4))
+    with pytest.raises(TypeError, match="Dion"):
+        StepGraph(torch.optim.SGD([param], lr=0.1))
+
+
 def test_workspace_release_resolves_the_current_gpu(monkeypatch) -> None:
     """``cuda`` names the current GPU: buffers kept under ``cuda:0`` are counted
     and released through ``cuda`` as well (an index-less device must not match
