@@ -221,6 +221,38 @@ def test_checkpoint_without_newton_schulz_kind_is_refused() -> None:
         opt.load_state_dict(state)
 
 
+def test_checkpoint_from_before_the_update_options_resumes_only_as_normuon() -> None:
+    """A checkpoint whose groups lack the row-normalization and momentum-form
+    keys is NorMuon with heavy-ball momentum: it resumes into that optimizer
+    (the next step bit-equal to the uninterrupted one) and is refused by a
+    Muon (reference tests/test_muon.py:318-342)."""
+    gen = torch.Generator().manual_seed(5)
+    w = nn.Parameter(_rand((64, 48), gen))
+    opt = _matrix_dion([w])
+    w.grad = _rand((64, 48), gen)
+    opt.step()
+    state = copy.deepcopy(opt.state_dict())
+    for group in state["param_groups"]:
+        del group["row_normalization"], group["momentum_form"]
+    twin = nn.Parameter(w.detach().clone())
+    resumed = _matrix_dion([twin])
+    resumed.load_state_dict(copy.deepcopy(state))
+    assert resumed.param_groups[0]["row_normalization"] == "normuon"
+    assert resumed.param_groups[0]["momentum_form"] == "heavy_ball"
+    grad = _rand((64, 48), gen)
+    w.grad, twin.grad = grad.clone(), grad.clone()
+    opt.step()
+    resumed.step()
+    assert torch.equal(twin.detach(), w.detach())
+    muon = Dion([{"params": [nn.Parameter(w.detach().clone())], ROUTE_KEY: "matrix",
+                  FRACTION_KEY: 1.0}], lr=LR, momentum=0.95, muon_beta2=0.95,
+                betas=(0.9, 0.99), weight_decay=0.0, eps=1e-8,
+                matrix_update=MatrixUpdate(NewtonSchulz.GRAM, RowNormalization.NONE,
+                                           MomentumForm.HEAVY_BALL))
+    with pytest.raises(ValueError, match="'row_normalization'"):
+        muon.load_state_dict(copy.deepcopy(state))
+
+
 def test_saved_state_keeps_one_storage_per_bucket(tmp_path) -> None:
     gen = torch.Generator().manual_seed(0)
     weights = [nn.Parameter(_rand((32, 32), gen)) for _ in range(2)]
