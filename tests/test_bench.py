@@ -1,7 +1,8 @@
 """bench.py's contract pieces that need no GPU (CPU).
 
-The FLOP convention of the Newton-Schulz TFLOP/s (the survey's F, not the
-MFMA work of the upper-tile products), the products' algorithmic bytes behind
+The FLOP convention of the Newton-Schulz TFLOP/s (F = 6 r^2 c + 23 r^3 for a
+wide Gram block, 15 r^2 c + 5 r^3 for the others; not the MFMA work of the
+upper-tile products), the products' algorithmic bytes behind
 roofline.traffic, and the refusal of more than one GPU.
 """
 
@@ -26,7 +27,7 @@ def test_ns_flops_convention() -> None:
     # r^3 and left product 2 r^2 c.
     assert bench.ns_flops(0, r, r) == 5 * (r * r * r + r**3 + 2 * r * r * r)
     assert bench.ns_flops(1, 1408, 2048) == 5 * (1408**2 * 2048 + 1408**3 + 2 * 1408**2 * 2048)
-    # Config 2 of the survey: 16 blocks 1024 x 4096, 0.8075 TFLOP.
+    # The gram-ns workload (the plugin call on 16 blocks 1024 x 4096): 0.8075 TFLOP.
     assert abs(16 * bench.ns_flops(0, 1024, 4096) / 1e12 - 0.8075) < 5e-4
 
 
