@@ -322,6 +322,98 @@ __global__ __launch_bounds__(256) void prepare_kernel(PrepArgs a) {
   }
 }
 
+// X = 16-bit(x / den) of a 16-bit input x (dionw_normalize_input): the
+// every-row prepare pass without momentum, with 8 columns per thread so that
+// loads and stores are 16 bytes per lane (a.vec: 8-element rows from a 16-byte
+// aligned address). The same arithmetic, padding and outputs as prepare_kernel.
+template <int ELEM, typename IN>
+__global__ __launch_bounds__(256) void prepare_input16_kernel(PrepArgs a) {
+  using T = typename std::conditional<ELEM == kF16, _Float16, __bf16>::type;
+  typedef IN in8 __attribute__((ext_vector_type(8)));
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  __shared__ T tile[kTile][kTile + 8];
+  const int tx = threadIdx.x & 7;   // 8 columns each
+  const int ty = threadIdx.x >> 3;  // rows ty + 32 i
+  const int64_t b = blockIdx.z;
+  const int64_t j0 = (int64_t)blockIdx.x * kTile + 8 * tx;
+  const int64_t p_base = (int64_t)blockIdx.y * kTile;
+  const float den = a.den[b];
+  const IN* x = reinterpret_cast<const IN*>(a.t.grad[0]) + b * a.rows * a.cols;
+
+  T vals[2][8];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t p = p_base + ty + 32 * i;
+    float u[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (p < a.k) {
+      const IN* row = x + p * a.cols;
+      if (a.vec && j0 + 7 < a.cols) {
+        const in8 v = __builtin_nontemporal_load(reinterpret_cast<const in8*>(row + j0));
+#pragma unroll
+        for (int c = 0; c < 8; ++c) u[c] = (float)v[c];
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (j0 + c < a.cols) u[c] = (float)row[j0 + c];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float q;
+      if (ELEM == kBF16) {
+        q = (float)(__bf16)u[c] / den;
+      } else {
+        q = u[c] / den;
+      }
+      vals[i][c] = (T)q;  // padding rows/cols hold u = 0 -> 0
+    }
+  }
+  T* out_r = a.out_r ? reinterpret_cast<T*>(a.out_r) + b * a.p_pad * a.j_pad : nullptr;
+  const bool store8 = (reinterpret_cast<uintptr_t>(a.out_r) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t p = p_base + ty + 32 * i;
+    if (out_r && p < a.p_pad) {
+      if (j0 + 7 < a.j_pad && store8) {
+        t8 v;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = vals[i][c];
+        *reinterpret_cast<t8*>(out_r + p * a.j_pad + j0) = v;
+      } else {
+        for (int c = 0; c < 8; ++c)
+          if (j0 + c < a.j_pad) out_r[p * a.j_pad + j0 + c] = vals[i][c];
+      }
+    }
+  }
+  if (a.out_t == nullptr) return;
+  // Transposed output [J_pad, P_pad] through LDS, read out as in prepare_kernel.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) tile[8 * tx + c][ty + 32 * i] = vals[i][c];
+  __syncthreads();
+  T* out_t = reinterpret_cast<T*>(a.out_t) + b * a.j_pad * a.p_pad;
+  const int jj = threadIdx.x >> 2;          // tile column -> output row
+  const int pp = (threadIdx.x & 3) * 16;    // 16 consecutive p
+  const int64_t j = (int64_t)blockIdx.x * kTile + jj;
+  if (j < a.j_pad) {
+    T* dst = out_t + j * a.p_pad + p_base + pp;
+    if (p_base + pp + 15 < a.p_pad) {
+      t8 v0, v1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v0[e] = tile[jj][pp + e];
+        v1[e] = tile[jj][pp + 8 + e];
+      }
+      reinterpret_cast<t8*>(dst)[0] = v0;
+      reinterpret_cast<t8*>(dst)[1] = v1;
+    } else {
+      for (int e = 0; e < 16; ++e)
+        if (p_base + pp + e < a.p_pad) dst[e] = tile[jj][pp + e];
+    }
+  }
+}
+
 // Raw fp32 copy of the input rows for a user-supplied orthogonalization
 // ([B, k, cols], no normalization), with the same momentum writes.
 __global__ __launch_bounds__(256) void prepare_raw_kernel(PrepArgs a) {
@@ -505,14 +597,19 @@ int dionw_normalize_input(const void* x, int32_t x_elem, int64_t blocks, int64_t
   a.vec = vec;
   const dim3 grid((unsigned)ceil_div(j_pad, kTile), (unsigned)ceil_div(p_pad, kTile),
                   (unsigned)blocks);
+  if (x_elem == kF32) {
+    if (elem == kF16) hipLaunchKernelGGL((prepare_kernel<kF16, float>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((prepare_kernel<kBF16, float>), grid, dim3(256), 0, stream, a);
+    return check_launch("normalize_input");
+  }
+  // 16-bit input: 8 columns per thread, 16-byte accesses where rows allow them.
+  a.vec = cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (elem == kF16) {
-    if (x_elem == kF32) hipLaunchKernelGGL((prepare_kernel<kF16, float>), grid, dim3(256), 0, stream, a);
-    else if (x_elem == kF16) hipLaunchKernelGGL((prepare_kernel<kF16, _Float16>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((prepare_kernel<kF16, __bf16>), grid, dim3(256), 0, stream, a);
+    if (x_elem == kF16) hipLaunchKernelGGL((prepare_input16_kernel<kF16, _Float16>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((prepare_input16_kernel<kF16, __bf16>), grid, dim3(256), 0, stream, a);
   } else {
-    if (x_elem == kF32) hipLaunchKernelGGL((prepare_kernel<kBF16, float>), grid, dim3(256), 0, stream, a);
-    else if (x_elem == kF16) hipLaunchKernelGGL((prepare_kernel<kBF16, _Float16>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((prepare_kernel<kBF16, __bf16>), grid, dim3(256), 0, stream, a);
+    if (x_elem == kF16) hipLaunchKernelGGL((prepare_input16_kernel<kBF16, _Float16>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((prepare_input16_kernel<kBF16, __bf16>), grid, dim3(256), 0, stream, a);
   }
   return check_launch("normalize_input");
 }

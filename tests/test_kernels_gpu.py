@@ -169,14 +169,21 @@ def test_prepare_row_major_only(elem: int, mode: str, blocks: int, rows: int, co
 
 @pytest.mark.parametrize("x_dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("elem", [0, 1], ids=["f16", "bf16"])
-@pytest.mark.parametrize(("blocks", "rows", "cols"), [(3, 64, 256), (2, 37, 300), (2, 9, 1001)])
+@pytest.mark.parametrize(("blocks", "rows", "cols", "offset"),
+                         [(3, 64, 256, 0), (2, 37, 300, 0), (2, 9, 1001, 0),
+                          # 16-byte rows with a partial last tile and padding rows
+                          (2, 100, 1032, 0), (1, 130, 4096, 0),
+                          # 16-byte rows from an address 8 bytes past a 16-byte boundary
+                          (2, 100, 1032, 4)])
 def test_normalize_input_reads_16bit_inputs(x_dtype, elem: int, blocks: int, rows: int,
-                                            cols: int) -> None:
+                                            cols: int, offset: int) -> None:
     """dionw_normalize_input on an fp16 / bf16 / fp32 input against
-    full_sumsq + block_denom + prepare_ns_input on its float32 copy (float4 and
+    full_sumsq + block_denom + prepare_ns_input on its float32 copy (vector and
     scalar paths): row sums, denominators and both outputs bit-identical."""
     g = _gen(12)
-    x = (torch.randn(blocks, rows, cols, generator=g) * 3).to(x_dtype).to(DEV)
+    n = blocks * rows * cols
+    flat = (torch.randn(n + offset, generator=g) * 3).to(x_dtype).to(DEV)
+    x = flat[offset:].view(blocks, rows, cols)
     src = x.float().contiguous()
     p_pad, j_pad = _round8(rows), _round8(cols)
     dtype = torch.float16 if elem == 0 else torch.bfloat16
